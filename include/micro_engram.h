@@ -1,0 +1,168 @@
+/*
+ * micro_engram.h -- C-ABI of the MI355X (gfx950) Engram lookup path.
+ *
+ * One shared library, libmicro_engram_amd.so, exports these entry points. They replace the
+ * torch-op bodies of micro-engram's hot path (reference files cited per function). Rules that
+ * hold for every entry point:
+ *
+ *   - Every tensor argument is a DEVICE pointer to memory the caller allocated, laid out
+ *     row-major and contiguous unless a stride argument says otherwise.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL = the null stream).
+ *     Nothing synchronises the host, nothing allocates device memory: a kernel that needs
+ *     scratch memory takes a caller-provided workspace whose size a *_workspace_size call
+ *     reports.
+ *   - The return value is ME_OK (0) or a negative ME_ERR_* code; me_last_error() returns
+ *     the message of the calling thread's last failure.
+ *   - The library is stateless and reentrant. Calls on different streams may overlap.
+ *
+ * Terms. A "table set" is the n_tables embedding tables of one engram, ordered order-major,
+ * head-minor (table k has n-gram order table_orders[k] and table_rows[k] rows of `dim`
+ * elements). `mults` is the engram's int64 [n_tables, max_order] hash-multiplier buffer.
+ */
+#ifndef MICRO_ENGRAM_H
+#define MICRO_ENGRAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------------------- */
+#define ME_OK 0
+#define ME_ERR_INVALID -1     /* bad argument (shape, size, null pointer, dtype) */
+#define ME_ERR_UNSUPPORTED -2 /* valid request this build has no kernel for */
+#define ME_ERR_HIP -3         /* the HIP runtime reported an error (launch, stream) */
+#define ME_ERR_WORKSPACE -4   /* workspace missing or smaller than *_workspace_size */
+
+/* ---- element types ------------------------------------------------------------------- */
+#define ME_I32 1
+#define ME_I64 2
+#define ME_F32 3
+#define ME_BF16 4
+#define ME_U8 5 /* bool masks */
+
+/* ---- gate modes (module.py:49-50) ---------------------------------------------------- */
+#define ME_GATE_SCALAR 0      /* sigmoid(rms(h) . rms(K) / sqrt(d)) */
+#define ME_GATE_SCALAR_SQRT 1 /* learnable RMSNorm scales + signed square root of the score */
+
+/* ---- limits -------------------------------------------------------------------------- */
+#define ME_MAX_TABLES 64
+#define ME_MAX_ORDER 8
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char *me_last_error(void);
+
+/* Library ABI version (bumped on any signature change). */
+int me_version(void);
+
+/*
+ * me_hash_ngrams -- n-gram row ids straight from token ids.
+ * Replaces MicroEngram.hash_ids (micro_engram/module.py:183-205).
+ *
+ *   input_ids      [batch, seq_len] of ids_dtype (ME_I32 / ME_I64)
+ *   position_ids   nullable; pos_dtype ME_I32/ME_I64; element (b, t) at
+ *                  position_ids[b * pos_batch_stride + t] (stride 0 broadcasts one row,
+ *                  like position_ids.expand_as(ids) in the reference)
+ *   canon          int64 [vocab]; ids are clamped to [0, vocab) before the lookup
+ *   mults          int64 [n_tables, max_order]
+ *   table_orders   HOST int32 [n_tables]; table_rows HOST int64 [n_tables]
+ *   idx_out        int64 [n_tables, batch * seq_len]: idx_out[k][b*seq_len+t] is the row of
+ *                  table k for the n-gram ending at (b, t)
+ *
+ * Token (b, t-i) enters the n-gram when t-i >= 0 and (no positions or position >= i);
+ * otherwise the raw pad_id does. Hash: (sum_i token_i * mults[k][i]) mod (2^31-1) mod rows,
+ * in wrapping int64 arithmetic with floor modulo, bit-exact with the reference.
+ */
+int me_hash_ngrams(const void *input_ids, int ids_dtype, int64_t batch, int64_t seq_len,
+                   const void *position_ids, int pos_dtype, int64_t pos_batch_stride,
+                   const int64_t *canon, int64_t vocab, const int64_t *mults, int32_t max_order,
+                   int32_t n_tables, const int32_t *table_orders, const int64_t *table_rows,
+                   int64_t pad_id, int64_t *idx_out, void *stream);
+
+/*
+ * me_hash_prev -- the same row ids from a [n, width] matrix of each token and its
+ * predecessors (column i = token at t-i, negative = missing, hashed as the raw pad_id).
+ * Replaces MicroEngram.hash_prev (micro_engram/module.py:207-226), the serving path fed by
+ * micro_engram_vllm/ids.py:10-59. Requires width >= max_order; rows are row_stride apart.
+ */
+int me_hash_prev(const void *ids, int ids_dtype, int64_t n, int64_t width, int64_t row_stride,
+                 const int64_t *canon, int64_t vocab, const int64_t *mults, int32_t max_order,
+                 int32_t n_tables, const int32_t *table_orders, const int64_t *table_rows,
+                 int64_t pad_id, int64_t *idx_out, void *stream);
+
+/*
+ * me_gather -- concatenated table rows for given row ids.
+ * Replaces MicroEngram.lookup + torch.cat (micro_engram/module.py:146-154, 233) and the
+ * TP=1 serving lookup micro_engram_vllm/tp.py:20-39: a row id outside [0, table_rows[k])
+ * yields a zero row, as the masked lookup there does.
+ *
+ *   idx     int64; row ids of table k for token i at idx[k * idx_table_stride + i]
+ *   tables  HOST array of n_tables device pointers, table k is [table_rows[k], dim]
+ *   mem     [n, n_tables * dim] of dtype (ME_BF16 / ME_F32): mem[i][k*dim + c] = tables[k][row][c]
+ */
+int me_gather(const int64_t *idx, int64_t idx_table_stride, int64_t n, int32_t n_tables,
+              const void *const *tables, const int64_t *table_rows, int32_t dim, int dtype,
+              void *mem, void *stream);
+
+/*
+ * me_hash_gather -- me_hash_ngrams fused with me_gather: one kernel reads the token ids,
+ * hashes every (token, table) pair and writes the token's concatenated memory vector.
+ * Replaces MicroEngram.forward's hash_ids + lookup + cat (module.py:263-265, 183-205,
+ * 146-154, 233). idx_out is nullable (row ids are written only when it is given).
+ */
+int me_hash_gather(const void *input_ids, int ids_dtype, int64_t batch, int64_t seq_len,
+                   const void *position_ids, int pos_dtype, int64_t pos_batch_stride,
+                   const int64_t *canon, int64_t vocab, const int64_t *mults, int32_t max_order,
+                   int32_t n_tables, const int32_t *table_orders, const int64_t *table_rows,
+                   int64_t pad_id, const void *const *tables, int32_t dim, int dtype, void *mem,
+                   int64_t *idx_out, void *stream);
+
+/*
+ * me_hash_prev_gather -- me_hash_prev fused with me_gather (serving decode / chunked
+ * prefill: module.py:207-226 then 146-154). idx_out is nullable.
+ */
+int me_hash_prev_gather(const void *ids, int ids_dtype, int64_t n, int64_t width,
+                        int64_t row_stride, const int64_t *canon, int64_t vocab,
+                        const int64_t *mults, int32_t max_order, int32_t n_tables,
+                        const int32_t *table_orders, const int64_t *table_rows, int64_t pad_id,
+                        const void *const *tables, int32_t dim, int dtype, void *mem,
+                        int64_t *idx_out, void *stream);
+
+/*
+ * me_gate_workspace_size -- bytes of workspace me_gate_residual needs for n tokens of
+ * model_dim (per-token partial sums of the gate, one triple per 256-column tile).
+ */
+int me_gate_workspace_size(int64_t n, int64_t model_dim, size_t *bytes);
+
+/*
+ * me_gate_residual -- key/value projection + scalar / scalar_sqrt gate + residual add.
+ * Replaces MicroEngram.inject after the lookup (micro_engram/module.py:239-261):
+ *
+ *   K = W_K mem, V = W_V mem        (engram dtype, fp32 accumulation, rounded to dtype)
+ *   h = rms_norm(hidden) [* (1 + q_scale_delta)], k = rms_norm(K) [* (1 + k_scale_delta)]
+ *   s = sum(h k) / sqrt(model_dim); ME_GATE_SCALAR_SQRT: s = sign(s) sqrt(max(|s|, 1e-6))
+ *   out = hidden + round_hidden(sigmoid(s) * V * keep)
+ *
+ *   hidden, out   [n, model_dim] of hidden_dtype (out may equal hidden: in-place is allowed)
+ *   mem           [n, mem_dim] of dtype; w_key, w_value [model_dim, mem_dim] of dtype
+ *                 (nn.Linear weights); mem_dim * element size must be a multiple of 16 bytes,
+ *                 model_dim a multiple of 8, every tensor 16-byte aligned
+ *   q/k_scale_delta  [model_dim] of scale_dtype, the stored scale - 1 (module.py:156-164);
+ *                 ignored for ME_GATE_SCALAR
+ *   keep          nullable [n] uint8 (bool): 0 leaves the token's hidden state unchanged
+ *   alpha_out     nullable [n] fp32: the gate value of each token (before keep)
+ *   workspace     at least me_gate_workspace_size(n, model_dim) bytes
+ */
+int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                     const void *mem, int64_t mem_dim, const void *w_key, const void *w_value,
+                     int dtype, const void *q_scale_delta, const void *k_scale_delta,
+                     int scale_dtype, int gate_mode, const uint8_t *keep, void *out,
+                     float *alpha_out, void *workspace, size_t workspace_size, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MICRO_ENGRAM_H */

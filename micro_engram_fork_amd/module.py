@@ -1,0 +1,343 @@
+"""MicroEngram for MI355X: the reference's module surface over the HIP kernels.
+
+Drop-in for micro_engram.module.MicroEngram (micro_engram/module.py:26-283): the same
+constructor, attributes (order_sizes, orders, _table_orders, table_rows, table_size), modules
+(tables, key, value, q_scale, k_scale / down, up), buffers (mults, canon), state-dict names and
+scale-as-delta conventions, and the same methods (hash_ids, hash_prev, lookup, inject, forward,
+norm_scales, shard_rows, all_parameters, pop_gate_stats). The compute of hash_ids / hash_prev /
+lookup / inject / forward runs in libmicro_engram_amd.so; tensors on the CPU raise instead of
+taking any other path.
+
+Differences from the reference, all deliberate:
+  * forward() fuses hashing and the row gather into one kernel (the reference's hash_ids +
+    lookup + cat), then one gate/residual op.
+  * lookup() returns views into one concatenated [N, n_tables * D] buffer instead of separate
+    tensors per table (same values).
+  * The HIP forward has no autograd formula yet: calling it where a gradient would be needed
+    raises instead of silently detaching. Use torch.no_grad() / torch.inference_mode().
+  * The "ple" gate keeps its parameters (so checkpoints load) but has no HIP kernel.
+"""
+import torch
+import torch.nn as nn
+
+from . import ops
+from ._lib import ME_GATE_SCALAR, ME_GATE_SCALAR_SQRT, ME_MAX_ORDER, ME_MAX_TABLES
+
+_PRIME = 2_147_483_647  # 2^31 - 1: the hash modulus (module.py:5)
+
+
+def resolve_order_sizes(table_size, orders=(2, 3), table_sizes=None):
+    """{order: rows per table}, sorted by order (module.py:8-23): every order in `orders` gets
+    `table_size`; `table_sizes` overrides or adds orders (keys may be strings); 0/None drops."""
+    sizes = {int(order): table_size for order in orders}
+    for order, rows in (table_sizes or {}).items():
+        sizes[int(order)] = rows
+    resolved = {order: int(rows) for order, rows in sorted(sizes.items()) if rows}
+    if not resolved:
+        raise ValueError("micro_engram: every n-gram order has size 0/None: nothing left to hash")
+    if min(resolved) < 1 or min(resolved.values()) < 1:
+        raise ValueError(f"micro_engram: bad orders/sizes {resolved}")
+    return resolved
+
+
+def _row_range(n_rows, rank, world):
+    """(first row, count) of `rank`'s share (micro_engram/rows.py:39-44)."""
+    per = -(-n_rows // world)
+    start = min(rank * per, n_rows)
+    return start, max(0, min(per, n_rows - start))
+
+
+class MicroEngram(nn.Module):
+    """Hashed n-gram memory added to the residual stream (micro_engram/module.py:26-47).
+
+    At position t the n-grams ending at t (orders in `orders`, `num_heads` hash functions
+    each) index per-(order, head) tables; the concatenated rows e feed a key/value projection,
+    and a scalar gate from rms(h) . rms(W_K e) decides how much of W_V e to add to h."""
+
+    GATES = ("scalar", "ple", "scalar_sqrt")
+    SCALAR_GATES = ("scalar", "scalar_sqrt")
+    DELTA_SCALES = ("q_scale", "k_scale")
+
+    row_shards = None     # per-table row shards (shard_rows), outside parameters()
+    row_info = None       # (rank, world, first row per table, rows per rank per table)
+    row_lookup_fn = None  # a server's own lookup for row-sharded tables
+
+    def __init__(self, model_dim, table_size=65_536, engram_dim=128, num_heads=4, orders=(2, 3),
+                 pad_id=0, seed=0, vocab_size=262_144, canon=None, gate="scalar",
+                 build_tables=True, table_sizes=None):
+        super().__init__()
+        if gate not in self.GATES:
+            raise ValueError(f"gate must be one of {self.GATES}, got {gate!r}")
+        self.gate = gate
+        self.order_sizes = resolve_order_sizes(table_size, orders, table_sizes)
+        self.orders = tuple(self.order_sizes)
+        self.engram_dim = engram_dim
+        self.seed = seed
+        self.pad_id = pad_id
+        # table k: order-major, head-minor (module.py:65-66)
+        self._table_orders = [order for order in self.orders for _ in range(num_heads)]
+        self.table_rows = [self.order_sizes[order] for order in self._table_orders]
+        self.table_size = self.table_rows[0] if len(set(self.table_rows)) == 1 else None
+        n_tables = len(self._table_orders)
+        if n_tables > ME_MAX_TABLES or max(self.orders) > ME_MAX_ORDER:
+            raise ValueError(f"[micro_engram] {n_tables} tables / order {max(self.orders)}: the HIP "
+                             f"kernels take at most {ME_MAX_TABLES} tables and order {ME_MAX_ORDER}")
+
+        if build_tables:
+            self.tables = nn.ModuleList(nn.Embedding(rows, engram_dim) for rows in self.table_rows)
+            for table in self.tables:
+                nn.init.normal_(table.weight, std=0.02)
+
+        mem_dim = engram_dim * n_tables
+        if gate in self.SCALAR_GATES:
+            self.key = nn.Linear(mem_dim, model_dim, bias=False)
+            self.value = nn.Linear(mem_dim, model_dim, bias=False)
+            nn.init.zeros_(self.value.weight)  # an untrained engram adds exactly nothing
+            if gate == "scalar_sqrt":
+                # stored as scale - 1 (module.py:81-87): bf16 cannot move 1.0 by an Adam step
+                self.q_scale = nn.Parameter(torch.zeros(model_dim))
+                self.k_scale = nn.Parameter(torch.zeros(model_dim))
+        else:
+            self.down = nn.Linear(model_dim, mem_dim, bias=False)
+            self.up = nn.Linear(mem_dim, model_dim, bias=False)
+            nn.init.zeros_(self.up.weight)
+
+        # Hash multipliers from torch's CPU generator, exactly as the reference draws them
+        # (module.py:93-99): the seed alone decides every row address.
+        gen = torch.Generator().manual_seed(seed)
+        mults = torch.randint(1, _PRIME, (n_tables, max(self.orders)), generator=gen,
+                              device="cpu") | 1
+        self.register_buffer("mults", mults)
+
+        if canon is None:
+            canon = torch.arange(vocab_size)
+        else:
+            canon = torch.as_tensor(canon).long().clone()
+            if canon.shape != (vocab_size,):
+                raise ValueError(f"canon must have shape ({vocab_size},), got {tuple(canon.shape)}")
+        self.register_buffer("canon", canon)
+
+    # ------------------------------------------------------------------ row shards (world = 1)
+    def shard_rows(self, rank, world, device=None, dtype=None, requires_grad=True, empty=False,
+                   pin_memory=False):
+        """Keep only `rank`'s rows of every table (module.py:115-138). On one GPU (world 1) this
+        is every row; the HIP lookup serves it directly. More ranks need the row exchange of
+        micro_engram/rows.py, which this build does not provide."""
+        spans = [_row_range(rows, rank, world) for rows in self.table_rows]
+        pers = [-(-rows // world) for rows in self.table_rows]
+        if "tables" in self._modules:
+            src = [t.weight.detach()[a:a + c] for t, (a, c) in zip(self.tables, spans)]
+            dtype = dtype or src[0].dtype
+            del self.tables
+        elif empty:
+            pin = pin_memory and torch.cuda.is_available()
+            src = [torch.empty(c, self.engram_dim, device=device, dtype=dtype, pin_memory=pin)
+                   for _, c in spans]
+        else:
+            gen = torch.Generator().manual_seed(self.seed * 1_000_003 + rank)
+            src = [torch.randn(c, self.engram_dim, generator=gen) * 0.02 for _, c in spans]
+        shards = [nn.Parameter(t if empty else t.to(device=device, dtype=dtype).clone(),
+                               requires_grad=requires_grad) for t in src]
+        self.__dict__["row_shards"] = shards
+        self.__dict__["row_info"] = (rank, world, [a for a, _ in spans], pers)
+        return shards
+
+    def all_parameters(self):
+        return list(self.parameters()) + list(self.row_shards or [])
+
+    def _table_weights(self):
+        """The full tables as [rows, D] tensors (module tables or world-1 row shards)."""
+        if self.row_shards is not None:
+            rank, world = self.row_info[0], self.row_info[1]
+            if world != 1:
+                raise NotImplementedError(
+                    f"[micro_engram] row-sharded tables over {world} ranks need the multi-GPU row "
+                    "exchange, which this single-GPU build does not provide")
+            return [s.detach() for s in self.row_shards]
+        return [t.weight.detach() for t in self.tables]
+
+    # ---------------------------------------------------------------- scales stored as deltas
+    def norm_scales(self):
+        """(q scale, k scale) in fp32: 1 + delta, the delta made fp32 first (module.py:161-164)."""
+        return 1 + self.q_scale.float(), 1 + self.k_scale.float()
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        for name in self.DELTA_SCALES:
+            key = prefix + name
+            if key in destination:  # files hold the scale itself, in fp32 (module.py:166-172)
+                destination[key] = destination[key].detach().float() + 1
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        for name in self.DELTA_SCALES:
+            key = prefix + name
+            if key in state_dict:
+                state_dict[key] = state_dict[key].float() - 1
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+
+    # ------------------------------------------------------------------------------- hashing
+    def _hash_consts(self, device):
+        canon = self.canon if self.canon.device == device else self.canon.to(device)
+        mults = self.mults if self.mults.device == device else self.mults.to(device)
+        return canon, mults
+
+    def hash_ids(self, input_ids, position_ids=None):
+        """Row ids of the n-grams ending at every position: list of n_tables LongTensors shaped
+        like input_ids [B, T] (module.py:183-205)."""
+        canon, mults = self._hash_consts(input_ids.device)
+        pos = position_ids.to(input_ids.device) if position_ids is not None else None
+        idx = ops.hash_ids(input_ids, pos, canon, mults, self._table_orders, self.table_rows,
+                           int(self.pad_id))
+        return list(idx.unbind(0))
+
+    def hash_prev(self, ids):
+        """Row ids from [N, W] ids of each token and its predecessors, -1 where missing: list of
+        n_tables LongTensors [N] (module.py:207-226)."""
+        canon, mults = self._hash_consts(ids.device)
+        idx = ops.hash_prev(ids, canon, mults, self._table_orders, self.table_rows,
+                            int(self.pad_id))
+        return list(idx.unbind(0))
+
+    # -------------------------------------------------------------------------------- lookup
+    @staticmethod
+    def _stacked_idx(idx):
+        """[n_tables, N] int64 view of the per-table ids: no copy when they are the rows of one
+        buffer (what hash_ids / hash_prev return), else a stacked copy."""
+        first = idx[0]
+        n = first.numel()
+        storage = first.untyped_storage().data_ptr()
+        if all(i.dtype == torch.int64 and i.is_contiguous() and i.numel() == n
+               and i.untyped_storage().data_ptr() == storage for i in idx):
+            if len(idx) == 1:
+                return first.reshape(1, n)
+            step = idx[1].data_ptr() - first.data_ptr()
+            if step % 8 == 0 and step // 8 >= n and all(
+                    i.data_ptr() - first.data_ptr() == k * step for k, i in enumerate(idx)):
+                return first.reshape(-1).as_strided((len(idx), n), (step // 8, 1))
+        return torch.stack([i.reshape(-1).long() for i in idx])
+
+    def _mem(self, idx):
+        if self.row_lookup_fn is not None and self.row_shards is not None:
+            return torch.cat(self.row_lookup_fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
+        return ops.gather(self._stacked_idx(idx), self._table_weights())
+
+    def lookup(self, idx):
+        """The table rows for the hashed ids: list of n_tables tensors [*idx shape, D]
+        (module.py:146-154)."""
+        shape = tuple(idx[0].shape)
+        mem = self._mem(idx)
+        D = self.engram_dim
+        return [mem[:, k * D:(k + 1) * D].reshape(*shape, D) for k in range(len(idx))]
+
+    # -------------------------------------------------------------------------------- inject
+    def _check_no_grad(self, hidden):
+        if torch.is_grad_enabled() and (hidden.requires_grad or any(
+                p.requires_grad for p in self.all_parameters())):
+            raise RuntimeError(
+                "[micro_engram] the HIP engram forward has no backward yet: run it under "
+                "torch.no_grad() / torch.inference_mode(), or freeze the engram's parameters")
+
+    def _gate(self, hidden, mem, keep):
+        if self.gate not in self.SCALAR_GATES:
+            raise NotImplementedError("[micro_engram] the 'ple' gate has no HIP kernel")
+        reader = self.key.weight
+        if mem.dtype != reader.dtype:
+            mem = mem.to(reader.dtype)  # rows stored in another dtype (module.py:234-238)
+        sqrt = self.gate == "scalar_sqrt"
+        outs = ops.gate_residual(
+            hidden, mem, self.key.weight.detach(), self.value.weight.detach(),
+            self.q_scale.detach() if sqrt else None, self.k_scale.detach() if sqrt else None,
+            ME_GATE_SCALAR_SQRT if sqrt else ME_GATE_SCALAR, keep, self.training)
+        if self.training:
+            self._record_gate(outs[1])
+        return outs[0]
+
+    def inject(self, hidden, idx, keep=None):
+        """hidden + gated memory of the rows `idx` (module.py:228-261); keep: optional [N] bool,
+        False leaves that token unchanged. Returns a new tensor."""
+        self._check_no_grad(hidden)
+        return self._gate(hidden, self._mem(idx), keep)
+
+    def forward(self, hidden, input_ids, position_ids=None):
+        """inject(hidden, hash_ids(input_ids, position_ids)) with hashing and gather fused into
+        one kernel (module.py:263-265)."""
+        self._check_no_grad(hidden)
+        if self.row_lookup_fn is not None and self.row_shards is not None:
+            return self.inject(hidden, self.hash_ids(input_ids.to(hidden.device), position_ids))
+        return self._gate(hidden, self.hashed_memory(input_ids, position_ids, hidden.device), None)
+
+    def hashed_memory(self, input_ids, position_ids=None, device=None):
+        """The concatenated memory vectors [B*T, n_tables * D] of every position: hash_ids +
+        lookup + cat (module.py:183-205, 146-154, 233) as one fused kernel."""
+        device = device or input_ids.device
+        input_ids = input_ids.to(device)
+        canon, mults = self._hash_consts(device)
+        pos = position_ids.to(device) if position_ids is not None else None
+        return ops.hash_gather(input_ids, pos, canon, mults, self._table_orders, self.table_rows,
+                               int(self.pad_id), self._table_weights(), False)[0]
+
+    def gate_residual(self, hidden, mem, keep=None):
+        """hidden + the gated projection of the memory vectors `mem` (module.py:239-261)."""
+        self._check_no_grad(hidden)
+        return self._gate(hidden, mem, keep)
+
+    # ------------------------------------------------------------------------- gate statistics
+    def _record_gate(self, alpha):
+        """Accumulates (sum of alpha, count, count of alpha > 0.99) on the device, no host sync
+        (module.py:268-274)."""
+        a = alpha.detach().float()
+        stats = getattr(self, "_gate_stats", None)
+        if stats is None or stats.device != a.device:
+            stats = torch.zeros(3, device=a.device)
+        self._gate_stats = stats + torch.stack([a.sum(), torch.tensor(float(a.numel()), device=a.device),
+                                                (a > 0.99).float().sum()])
+
+    def pop_gate_stats(self):
+        """(mean gate, fraction of tokens with gate > 0.99) since the last call, or None."""
+        stats = getattr(self, "_gate_stats", None)
+        self._gate_stats = None
+        if stats is None or stats[1] == 0:
+            return None
+        s, n, sat = stats.tolist()
+        return s / n, sat / n
+
+
+def engram_from_spec(spec, model_dim, vocab_size, pad_default=0, canon=None, build_tables=True):
+    """A MicroEngram from one engram spec dict (module.py:299-315); the seed decides every hash
+    address, so it is taken from the spec."""
+    return MicroEngram(
+        model_dim=model_dim,
+        table_size=spec["table_size"],
+        table_sizes=spec.get("table_sizes"),
+        engram_dim=spec["engram_dim"],
+        num_heads=spec["num_heads"],
+        orders=tuple(spec.get("orders") or (2, 3)),
+        pad_id=spec["pad_id"] if spec.get("pad_id") is not None else pad_default,
+        seed=spec.get("seed") or 0,
+        vocab_size=vocab_size,
+        canon=canon,
+        gate=spec.get("gate") or "scalar",
+        build_tables=build_tables,
+    )
+
+
+def check_loaded(engram, sd, where):
+    """Load `sd` into `engram`, refusing multipliers that differ from the seed's
+    (module.py:318-328)."""
+    if "mults" in sd and not torch.equal(sd["mults"].to(engram.mults.device).long(), engram.mults.long()):
+        raise ValueError(f"[micro_engram] {where}: the saved hash multipliers differ from the ones "
+                         f"this engram's seed gives; the seed is wrong for these weights")
+    result = engram.load_state_dict(sd, strict=False)
+    problems = [k for k in result.missing_keys if k != "mults"] + list(result.unexpected_keys)
+    if problems:
+        raise ValueError(f"[micro_engram] {where} does not match the engram settings: {problems[:10]}")
+    return result
+
+
+SEED_STRIDE = 10007  # default seed of the engram at layer L is SEED_STRIDE * L (weights.py:157)
+
+
+def default_seed(layer):
+    return SEED_STRIDE * int(layer)

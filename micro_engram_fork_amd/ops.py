@@ -1,0 +1,291 @@
+"""torch custom ops over the C-ABI of libmicro_engram_amd.so.
+
+Each op takes device tensors, allocates its outputs with torch (the library never allocates),
+and enqueues the HIP kernels on the current stream. Ops are registered with
+torch.library.custom_op plus a fake implementation, so torch.compile and CUDA-graph capture see
+shape-only functions with no host synchronisation (the reference's own custom-op idiom,
+micro_engram/train/vendor/op_registry.py:40-67). CPU tensors raise: there is no CPU path.
+"""
+import ctypes
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import ME_BF16, ME_F32, ME_I32, ME_I64, ME_U8, call, i32_array, i64_array, ptr_array
+
+_DTYPES = {torch.int32: ME_I32, torch.int64: ME_I64, torch.float32: ME_F32,
+           torch.bfloat16: ME_BF16, torch.bool: ME_U8, torch.uint8: ME_U8}
+
+
+def dtype_code(t):
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"[micro_engram] unsupported dtype {t.dtype}") from None
+
+
+def require_gpu(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"[micro_engram] the engram path runs only on the GPU (HIP kernels); got a tensor on "
+                f"{t.device}. Move the engram and its inputs to a GPU.")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"[micro_engram] tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def stream_of(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------------------------ hashing
+def _pos_arg(position_ids, batch, seq_len):
+    """(tensor, batch stride) for position_ids broadcast like .expand_as(ids) in module.py:195."""
+    if position_ids is None:
+        return None, 0
+    pos = position_ids
+    if pos.dim() == 1:
+        pos = pos.unsqueeze(0)
+    if pos.dim() != 2 or pos.shape[-1] != seq_len or pos.shape[0] not in (1, batch):
+        raise ValueError(f"[micro_engram] position_ids of shape {tuple(position_ids.shape)} do not "
+                         f"broadcast to the ids' [{batch}, {seq_len}]")
+    if pos.dtype not in (torch.int32, torch.int64):
+        pos = pos.long()
+    pos = pos.contiguous()
+    return pos, (0 if pos.shape[0] == 1 else seq_len)
+
+
+def _ids2d(input_ids):
+    if input_ids.dim() != 2:
+        raise ValueError(f"[micro_engram] input_ids must be [batch, seq], got {tuple(input_ids.shape)}")
+    ids = input_ids if input_ids.dtype in (torch.int32, torch.int64) else input_ids.long()
+    return ids.contiguous()
+
+
+def _table_args(table_orders, table_rows):
+    return len(table_orders), i32_array(list(table_orders)), i64_array(list(table_rows))
+
+
+@torch.library.custom_op("micro_engram_amd::hash_ids", mutates_args=())
+def hash_ids(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], canon: torch.Tensor,
+             mults: torch.Tensor, table_orders: List[int], table_rows: List[int],
+             pad_id: int) -> torch.Tensor:
+    """Row ids int64 [n_tables, B, T] (micro_engram/module.py:183-205)."""
+    dev = require_gpu(input_ids, position_ids, canon, mults)
+    ids = _ids2d(input_ids)
+    B, T = ids.shape
+    pos, pstride = _pos_arg(position_ids, B, T)
+    nt, orders, rows = _table_args(table_orders, table_rows)
+    out = torch.empty((nt, B, T), dtype=torch.int64, device=dev)
+    call("me_hash_ngrams", ids.data_ptr(), dtype_code(ids), B, T, _p(pos),
+         dtype_code(pos) if pos is not None else 0, pstride, canon.data_ptr(), canon.numel(),
+         mults.data_ptr(), mults.shape[1], nt, orders, rows, pad_id, out.data_ptr(), stream_of(dev))
+    return out
+
+
+@hash_ids.register_fake
+def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id):
+    return input_ids.new_empty((len(table_orders), *input_ids.shape), dtype=torch.int64)
+
+
+def _prev_ids(ids):
+    if ids.dim() != 2:
+        raise ValueError(f"[micro_engram] ids must be [n, max_order], got {tuple(ids.shape)}")
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.long()
+    if ids.stride(1) != 1:
+        ids = ids.contiguous()
+    return ids
+
+
+@torch.library.custom_op("micro_engram_amd::hash_prev", mutates_args=())
+def hash_prev(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
+              table_orders: List[int], table_rows: List[int], pad_id: int) -> torch.Tensor:
+    """Row ids int64 [n_tables, N] from [N, W] predecessor ids (micro_engram/module.py:207-226)."""
+    dev = require_gpu(ids, canon, mults)
+    ids = _prev_ids(ids)
+    N, W = ids.shape
+    nt, orders, rows = _table_args(table_orders, table_rows)
+    out = torch.empty((nt, N), dtype=torch.int64, device=dev)
+    call("me_hash_prev", ids.data_ptr(), dtype_code(ids), N, W, ids.stride(0) if N else W,
+         canon.data_ptr(), canon.numel(), mults.data_ptr(), mults.shape[1], nt, orders, rows,
+         pad_id, out.data_ptr(), stream_of(dev))
+    return out
+
+
+@hash_prev.register_fake
+def _(ids, canon, mults, table_orders, table_rows, pad_id):
+    return ids.new_empty((len(table_orders), ids.shape[0]), dtype=torch.int64)
+
+
+# ------------------------------------------------------------------------------------- gather
+def _tables_arg(tables: Sequence[torch.Tensor]):
+    t0 = tables[0]
+    dim = t0.shape[1]
+    for t in tables:
+        if t.dim() != 2 or t.shape[1] != dim or t.dtype != t0.dtype:
+            raise ValueError("[micro_engram] tables must be 2-D with one row width and dtype")
+        if not t.is_contiguous():
+            raise ValueError("[micro_engram] tables must be contiguous")
+    return ptr_array([t.data_ptr() for t in tables]), i64_array([t.shape[0] for t in tables]), dim
+
+
+@torch.library.custom_op("micro_engram_amd::gather", mutates_args=())
+def gather(idx: torch.Tensor, tables: List[torch.Tensor]) -> torch.Tensor:
+    """mem [N, n_tables * D] from row ids int64 [n_tables, N] (module.py:146-154, 233; rows
+    outside a table read as zeros, micro_engram_vllm/tp.py:20-39)."""
+    dev = require_gpu(idx, *tables)
+    if idx.dim() != 2 or idx.shape[0] != len(tables) or idx.dtype != torch.int64:
+        raise ValueError("[micro_engram] idx must be int64 [n_tables, N]")
+    if idx.stride(1) != 1:
+        idx = idx.contiguous()
+    ptrs, rows, dim = _tables_arg(tables)
+    N = idx.shape[1]
+    mem = torch.empty((N, len(tables) * dim), dtype=tables[0].dtype, device=dev)
+    call("me_gather", idx.data_ptr(), idx.stride(0) if len(tables) > 1 else N, N, len(tables),
+         ptrs, rows, dim, dtype_code(tables[0]), mem.data_ptr(), stream_of(dev))
+    return mem
+
+
+@gather.register_fake
+def _(idx, tables):
+    return tables[0].new_empty((idx.shape[1], len(tables) * tables[0].shape[1]))
+
+
+@torch.library.custom_op("micro_engram_amd::hash_gather", mutates_args=())
+def hash_gather(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], canon: torch.Tensor,
+                mults: torch.Tensor, table_orders: List[int], table_rows: List[int], pad_id: int,
+                tables: List[torch.Tensor], with_idx: bool) -> List[torch.Tensor]:
+    """[mem [B*T, n_tables*D]] or [mem, idx [n_tables, B, T]]: hash_ids + lookup + cat in one
+    kernel (module.py:263-265)."""
+    dev = require_gpu(input_ids, position_ids, canon, mults, *tables)
+    ids = _ids2d(input_ids)
+    B, T = ids.shape
+    pos, pstride = _pos_arg(position_ids, B, T)
+    nt, orders, rows = _table_args(table_orders, table_rows)
+    ptrs, _rows, dim = _tables_arg(tables)
+    mem = torch.empty((B * T, nt * dim), dtype=tables[0].dtype, device=dev)
+    idx = torch.empty((nt, B, T), dtype=torch.int64, device=dev) if with_idx else None
+    call("me_hash_gather", ids.data_ptr(), dtype_code(ids), B, T, _p(pos),
+         dtype_code(pos) if pos is not None else 0, pstride, canon.data_ptr(), canon.numel(),
+         mults.data_ptr(), mults.shape[1], nt, orders, rows, pad_id, ptrs, dim,
+         dtype_code(tables[0]), mem.data_ptr(), _p(idx), stream_of(dev))
+    return [mem, idx] if with_idx else [mem]
+
+
+@hash_gather.register_fake
+def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id, tables, with_idx):
+    n = input_ids.shape[0] * input_ids.shape[1]
+    mem = tables[0].new_empty((n, len(tables) * tables[0].shape[1]))
+    if with_idx:
+        return [mem, input_ids.new_empty((len(tables), *input_ids.shape), dtype=torch.int64)]
+    return [mem]
+
+
+@torch.library.custom_op("micro_engram_amd::hash_prev_gather", mutates_args=())
+def hash_prev_gather(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
+                     table_orders: List[int], table_rows: List[int], pad_id: int,
+                     tables: List[torch.Tensor], with_idx: bool) -> List[torch.Tensor]:
+    """[mem [N, n_tables*D]] or [mem, idx [n_tables, N]]: hash_prev + lookup in one kernel."""
+    dev = require_gpu(ids, canon, mults, *tables)
+    ids = _prev_ids(ids)
+    N, W = ids.shape
+    nt, orders, rows = _table_args(table_orders, table_rows)
+    ptrs, _rows, dim = _tables_arg(tables)
+    mem = torch.empty((N, nt * dim), dtype=tables[0].dtype, device=dev)
+    idx = torch.empty((nt, N), dtype=torch.int64, device=dev) if with_idx else None
+    call("me_hash_prev_gather", ids.data_ptr(), dtype_code(ids), N, W, ids.stride(0) if N else W,
+         canon.data_ptr(), canon.numel(), mults.data_ptr(), mults.shape[1], nt, orders, rows,
+         pad_id, ptrs, dim, dtype_code(tables[0]), mem.data_ptr(), _p(idx), stream_of(dev))
+    return [mem, idx] if with_idx else [mem]
+
+
+@hash_prev_gather.register_fake
+def _(ids, canon, mults, table_orders, table_rows, pad_id, tables, with_idx):
+    mem = tables[0].new_empty((ids.shape[0], len(tables) * tables[0].shape[1]))
+    if with_idx:
+        return [mem, ids.new_empty((len(tables), ids.shape[0]), dtype=torch.int64)]
+    return [mem]
+
+
+# ----------------------------------------------------------------------------- gate + residual
+def gate_workspace_bytes(n, d):
+    size = ctypes.c_size_t(0)
+    call("me_gate_workspace_size", n, d, ctypes.byref(size))
+    return size.value
+
+
+def _aligned(t):
+    return t.data_ptr() % 16 == 0
+
+
+@torch.library.custom_op("micro_engram_amd::gate_residual", mutates_args=())
+def gate_residual(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
+                  w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
+                  k_scale_delta: Optional[torch.Tensor], gate_mode: int,
+                  keep: Optional[torch.Tensor], with_alpha: bool) -> List[torch.Tensor]:
+    """[out] or [out, alpha [N] fp32]: hidden + gated W_V mem, the scalar gates of
+    MicroEngram.inject (micro_engram/module.py:239-261). hidden [..., d]; mem [N, M] with N the
+    number of hidden rows; weights [d, M] (nn.Linear layout) in mem's dtype."""
+    dev = require_gpu(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, keep)
+    d = hidden.shape[-1]
+    x = hidden.reshape(-1, d)
+    N = x.shape[0]
+    if mem.dim() != 2 or mem.shape[0] != N:
+        raise ValueError(f"[micro_engram] mem {tuple(mem.shape)} does not match {N} tokens")
+    M = mem.shape[1]
+    for w in (w_key, w_value):
+        if tuple(w.shape) != (d, M) or w.dtype != mem.dtype:
+            raise ValueError(f"[micro_engram] weight {tuple(w.shape)}/{w.dtype} does not match "
+                             f"[{d}, {M}]/{mem.dtype}")
+    x, mem = x.contiguous(), mem.contiguous()
+    w_key, w_value = w_key.contiguous(), w_value.contiguous()
+    if not all(_aligned(t) for t in (x, mem, w_key, w_value)):
+        x, mem, w_key, w_value = (t.clone() if not _aligned(t) else t for t in (x, mem, w_key, w_value))
+    scale_code = 0
+    if gate_mode == _lib.ME_GATE_SCALAR_SQRT:
+        if q_scale_delta is None or k_scale_delta is None:
+            raise ValueError("[micro_engram] the scalar_sqrt gate needs q_scale and k_scale")
+        q_scale_delta, k_scale_delta = q_scale_delta.contiguous(), k_scale_delta.contiguous()
+        if q_scale_delta.dtype != k_scale_delta.dtype:
+            k_scale_delta = k_scale_delta.to(q_scale_delta.dtype)
+        scale_code = dtype_code(q_scale_delta)
+    keep_u8 = None
+    if keep is not None:
+        keep_u8 = keep.reshape(-1).to(torch.uint8).contiguous()
+        if keep_u8.numel() != N:
+            raise ValueError(f"[micro_engram] keep has {keep_u8.numel()} entries for {N} tokens")
+    out = torch.empty_like(x)
+    alpha = torch.empty(N, dtype=torch.float32, device=dev) if with_alpha else None
+    ws = torch.empty(max(gate_workspace_bytes(N, d), 16), dtype=torch.uint8, device=dev)
+    call("me_gate_residual", x.data_ptr(), dtype_code(x), N, d, mem.data_ptr(), M,
+         w_key.data_ptr(), w_value.data_ptr(), dtype_code(mem), _p(q_scale_delta),
+         _p(k_scale_delta), scale_code, gate_mode, _p(keep_u8), out.data_ptr(), _p(alpha),
+         ws.data_ptr(), ws.numel(), stream_of(dev))
+    out = out.reshape(hidden.shape)
+    return [out, alpha] if with_alpha else [out]
+
+
+@gate_residual.register_fake
+def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha):
+    out = torch.empty_like(hidden)
+    if with_alpha:
+        return [out, hidden.new_empty((hidden.numel() // hidden.shape[-1],), dtype=torch.float32)]
+    return [out]
+
+
+def library_loaded():
+    """Loads the HIP library (raises if it is missing) and returns its path."""
+    _lib.load()
+    return _lib.lib_path()

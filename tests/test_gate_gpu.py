@@ -1,0 +1,195 @@
+"""Stage 3 (key/value projection + scalar gates + residual) and the whole forward on the GPU
+against the oracle's torch-CPU restatement of MicroEngram.inject (module.py:228-261).
+
+Tolerances (stated per dtype, checked per element):
+  fp32  |gpu - ref| <= 1e-5 * rms(hidden row)
+  bf16  |gpu - ref| <= 1 bf16 ulp of the output + 2^-6 * |ref - hidden| : one rounding step of
+        the residual add plus the effect of a one-ulp flip in the bf16 K/V products;
+        and per row max|gpu - ref| <= 1e-2 * ||hidden row||_2
+  gate  |alpha_gpu - alpha_ref| <= 1e-5 (fp32) / 2e-3 (bf16)
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from micro_engram_fork_amd import MicroEngram, ops, synthetic
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bf16_ulp(x):
+    x = x.abs().float().clamp_min(2.0 ** -126)
+    return torch.pow(2.0, torch.floor(torch.log2(x)) - 7)
+
+
+def assert_close_out(got, ref, hidden, dtype):
+    got, ref, hidden = got.float().cpu(), ref.float().cpu(), hidden.float().cpu()
+    got, ref, hidden = (t.reshape(-1, t.shape[-1]) for t in (got, ref, hidden))
+    err = (got - ref).abs()
+    if dtype == torch.float32:
+        rms = hidden.pow(2).mean(-1, keepdim=True).sqrt()
+        bad = err > 1e-5 * rms + 1e-30
+    else:
+        bound = _bf16_ulp(torch.maximum(got.abs(), ref.abs())) + 2.0 ** -6 * (ref - hidden).abs()
+        bad = err > bound
+        row_norm = hidden.norm(dim=-1)
+        assert (err.max(dim=-1).values <= 1e-2 * row_norm).all()
+    assert not bad.any(), f"{int(bad.sum())} elements out of tolerance, max err {float(err.max()):.3g}"
+
+
+def _make(dtype, gate="scalar_sqrt", d=32, dim=4, heads=2, orders=(2, 3), sizes=None, seed=0):
+    eng = MicroEngram(model_dim=d, table_size=257, engram_dim=dim, num_heads=heads, orders=orders,
+                      table_sizes=sizes, vocab_size=1000, gate=gate, seed=seed)
+    synthetic.fill_dense(eng, seed=seed, std=0.2)
+    return eng.to(device=DEV, dtype=dtype).eval()
+
+
+def _oracle_forward(eng, hidden, ids, pos=None, keep=None):
+    idx = oracle.hash_ids(ids.cpu().numpy(), eng.mults.cpu().numpy(), eng._table_orders,
+                          eng.table_rows, eng.canon.cpu().numpy(), eng.pad_id,
+                          position_ids=None if pos is None else pos.cpu().numpy())
+    tables = [t.weight.detach().cpu().float().numpy() for t in eng.tables]
+    mem = torch.from_numpy(oracle.lookup(tables, list(idx.reshape(idx.shape[0], -1))))
+    mem = mem.to(eng.key.weight.dtype)
+    sqrt = eng.gate == "scalar_sqrt"
+    d = hidden.shape[-1]
+    return oracle.inject(hidden.cpu().reshape(-1, d), mem, eng.key.weight.detach().cpu(),
+                         eng.value.weight.detach().cpu(), eng.gate,
+                         eng.q_scale.detach().cpu() if sqrt else None,
+                         eng.k_scale.detach().cpu() if sqrt else None,
+                         keep=None if keep is None else keep.cpu().reshape(-1), return_alpha=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("gate", ["scalar_sqrt", "scalar"])
+def test_forward_small(dtype, gate):
+    torch.manual_seed(0)
+    eng = _make(dtype, gate)
+    ids = torch.randint(5, 1000, (2, 12), device=DEV)
+    hidden = (torch.randn(2, 12, 32) * 50).to(dtype).to(DEV)
+    with torch.no_grad():
+        out = eng(hidden, ids)
+    ref, _ = _oracle_forward(eng, hidden, ids)
+    assert out.dtype == dtype and out.shape == hidden.shape
+    assert_close_out(out, ref.reshape(out.shape), hidden, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gate_alpha_matches(dtype):
+    torch.manual_seed(1)
+    eng = _make(dtype, d=64, dim=8, heads=2, orders=(2, 3, 4))
+    ids = torch.randint(0, 1000, (1, 300), device=DEV)
+    hidden = torch.randn(1, 300, 64).to(dtype).to(DEV)
+    idx = eng.hash_ids(ids)
+    mem = torch.cat(eng.lookup(idx), dim=-1).reshape(300, -1)
+    with torch.no_grad():
+        out, alpha = ops.gate_residual(hidden, mem, eng.key.weight, eng.value.weight, eng.q_scale,
+                                       eng.k_scale, 1, None, True)
+    ref, ref_alpha = _oracle_forward(eng, hidden, ids)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert (alpha.cpu() - ref_alpha).abs().max() <= tol
+    assert_close_out(out, ref.reshape(out.shape), hidden, dtype)
+
+
+def test_step0_is_exact_noop():
+    # value weight zero (a fresh engram): output == input exactly (test_gate.py:24-27)
+    for dtype in (torch.float32, torch.bfloat16):
+        eng = MicroEngram(model_dim=32, table_size=257, engram_dim=4, num_heads=2, vocab_size=1000,
+                          gate="scalar_sqrt").to(device=DEV, dtype=dtype)
+        hidden = (torch.randn(2, 12, 32) * 50).to(dtype).to(DEV)
+        with torch.no_grad():
+            out = eng(hidden, torch.randint(5, 1000, (2, 12), device=DEV))
+        assert torch.equal(out, hidden)
+
+
+def test_keep_mask():
+    # keep=False rows unchanged, keep=True rows as without the mask (test_gate.py:122-130)
+    eng = _make(torch.float32)
+    ids = torch.randint(5, 1000, (2, 12), device=DEV)
+    hidden = (torch.randn(2, 12, 32) * 50).to(DEV)
+    keep = torch.tensor([[True] * 6 + [False] * 6] * 2, device=DEV)
+    with torch.no_grad():
+        idx = eng.hash_ids(ids)
+        masked, full = eng.inject(hidden, idx, keep), eng.inject(hidden, idx)
+    assert torch.equal(masked[:, 6:], hidden[:, 6:])
+    assert torch.equal(masked[:, :6], full[:, :6])
+
+
+def test_inject_does_not_modify_hidden():
+    eng = _make(torch.bfloat16)
+    hidden = torch.randn(5, 32, device=DEV).to(torch.bfloat16)
+    before = hidden.clone()
+    with torch.no_grad():
+        eng.inject(hidden, eng.hash_prev(torch.randint(-1, 1000, (5, 3), device=DEV)))
+    assert torch.equal(hidden, before)
+
+
+def test_gate_stats_recorded_in_training_mode():
+    eng = _make(torch.float32).train()
+    with torch.no_grad():
+        eng(torch.randn(1, 40, 32, device=DEV), torch.randint(0, 1000, (1, 40), device=DEV))
+    mean, sat = eng.pop_gate_stats()
+    assert 0.0 < mean < 1.0 and 0.0 <= sat <= 1.0
+    eng.eval()
+    with torch.no_grad():
+        eng(torch.randn(1, 40, 32, device=DEV), torch.randint(0, 1000, (1, 40), device=DEV))
+    assert eng.pop_gate_stats() is None
+
+
+def test_grad_mode_raises():
+    eng = _make(torch.float32)
+    with pytest.raises(RuntimeError, match="no backward"):
+        eng(torch.randn(1, 4, 32, device=DEV), torch.randint(0, 1000, (1, 4), device=DEV))
+
+
+def test_golden_inject_fixture():
+    import os
+
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "inject_small.npz"))
+    t = {k: torch.from_numpy(f[k]).to(DEV) for k in f.files}
+    with torch.no_grad():
+        out, alpha = ops.gate_residual(t["hidden"], t["mem"], t["wk"], t["wv"], t["dq"], t["dk"], 1,
+                                       None, True)
+    assert (alpha.cpu() - torch.from_numpy(f["alpha"])).abs().max() <= 1e-5
+    assert_close_out(out, torch.from_numpy(f["out"]), t["hidden"], torch.float32)
+
+
+@pytest.mark.parametrize("n,d,dim,heads", [(300, 264, 8, 3), (513, 1024, 16, 2), (7, 4096, 64, 8)])
+def test_ragged_shapes_bf16(n, d, dim, heads):
+    # token counts and model dims that are not multiples of the 256 tile
+    torch.manual_seed(n)
+    eng = _make(torch.bfloat16, d=d, dim=dim, heads=heads, orders=(2, 3, 4))
+    ids = torch.randint(0, 1000, (1, n), device=DEV)
+    hidden = torch.randn(1, n, d).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        out = eng(hidden, ids)
+    ref, _ = _oracle_forward(eng, hidden, ids)
+    assert_close_out(out, ref.reshape(out.shape), hidden, torch.bfloat16)
+
+
+def test_tiny_forward_fp32_full():
+    eng = synthetic.build_engram("tiny", DEV, seed=0).eval()
+    ids, pos, hidden = synthetic.tiny_inputs(seed=0, device=DEV)
+    with torch.no_grad():
+        out = eng(hidden, ids, pos)
+    ref, _ = _oracle_forward(eng, hidden, ids, pos)
+    assert_close_out(out, ref.reshape(out.shape), hidden, torch.float32)
+
+
+def test_gemma_prefill_forward_sampled():
+    eng = synthetic.build_engram("gemma", DEV, seed=0).eval()
+    ids, pos, hidden = synthetic.prefill_inputs(seed=0, device=DEV)
+    with torch.no_grad():
+        out = eng(hidden, ids, pos)
+        idx = torch.stack(eng.hash_ids(ids, pos)).reshape(len(eng.tables), -1)
+    sample = torch.from_numpy(np.random.Generator(np.random.PCG64(1)).choice(8192, 256, replace=False)).to(DEV)
+    mem = torch.cat([t.weight[idx[k][sample]] for k, t in enumerate(eng.tables)], dim=-1).cpu()
+    h = hidden.reshape(-1, hidden.shape[-1])[sample].cpu()
+    ref = oracle.inject(h, mem, eng.key.weight.detach().cpu(), eng.value.weight.detach().cpu(),
+                        "scalar_sqrt", eng.q_scale.detach().cpu(), eng.k_scale.detach().cpu())
+    got = out.reshape(-1, out.shape[-1])[sample]
+    assert_close_out(got, ref, h, torch.bfloat16)
+    del eng
+    torch.cuda.empty_cache()
