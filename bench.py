@@ -10,7 +10,8 @@ all inputs already in HBM. Prints one JSON line:
 
   value         forward tokens/s over the K timed steps (wall clock, synchronised)
   roofline      the gather kernel (the metric's HBM figure): algorithmic bytes per launch /
-                its mean duration from HIP events on the launch stream, against 8 TB/s
+                its mean duration (launches captured in a HIP graph, replayed between two HIP
+                events on the replay stream), against 8 TB/s
   roofline_gate the K/V projection kernels: 4 * M * d FLOP per token / their mean duration,
                 against 2.5 PFLOP/s dense bf16
   cpu_baseline  the oracle's torch-CPU forward on a token sample of the same batch
@@ -103,31 +104,47 @@ def main():
     ids, pos, hidden = synthetic.prefill_inputs(seed=0, device=dev)
     T = ids.numel()
 
-    def step(ev=None):
+    def step():
         mem = eng.hashed_memory(ids, pos, dev)
-        if ev is not None:
-            ev[1].record()
-        out = eng.gate_residual(hidden, mem)
-        return out
+        return eng.gate_residual(hidden, mem)
+
+    def kernel_ms(fn, reps):
+        """Mean duration of `fn`'s kernels: `reps` calls captured in one HIP graph, replayed
+        between two HIP events on the replay stream (graph replay keeps host dispatch out of
+        the measurement)."""
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(reps):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(side)
+            graph.replay()
+            end.record(side)
+            torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
 
     with torch.inference_mode():
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
-        # timed region: K forward steps; HIP events bracket the gather and gate kernels of
-        # every step on the launch stream
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-        torch.cuda.synchronize()
+        # timed region: K whole forward steps, synchronised on both sides
         t0 = time.perf_counter()
-        for k in range(args.steps):
-            evs[k][0].record()
-            step(evs[k])
-            evs[k][2].record()
+        for _ in range(args.steps):
+            step()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        # per-kernel timing of the two stages on the same inputs
+        mem = eng.hashed_memory(ids, pos, dev)
+        gather_ms = kernel_ms(lambda: eng.hashed_memory(ids, pos, dev), 20)
+        gate_ms = kernel_ms(lambda: eng.gate_residual(hidden, mem), 10)
 
-    gather_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    gate_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
     esize = eng.tables[0].weight.element_size()
     gbytes = gather_bytes_per_token(eng, esize) * T
     gather_gbs = gbytes / (gather_ms * 1e-3) / 1e9

@@ -19,31 +19,45 @@
 //
 // GEMM tiling: a 256-thread workgroup owns a 256 (model dims j) x 256 (tokens n) output tile;
 // its four waves each hold 128 x 128 as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (fp32 engrams:
-// v_mfma_f32_32x32x2f32). Both operands are K-contiguous in HBM (W is [d, M], mem is [N, M]),
-// so each k-step is one 16-byte load per lane for A and for B. The K loop moves 128 bytes of K
-// per row per step through a double-buffered LDS tile (2 x 64 KiB) whose 16-byte chunks are
-// XOR-swizzled by (row & 7): a wave's ds_read_b128 of 32 rows at one k then hits distinct
-// banks in every 8-lane group. Workgroup ids are remapped so the 32 CUs of one XCD work on a
-// compact group of tiles (8 token tiles x 4 column tiles) and share their operands in that
-// XCD's L2.
+// v_mfma_f32_32x32x2f32). Both operands are K-contiguous in HBM (W is [d, M], mem is [N, M]).
+// The K loop streams 64-byte k-slabs of all 256 A rows and 256 B rows through a 5-slot LDS
+// ring (5 x 32 KiB): buffer_load ... lds moves each 16-byte chunk straight from memory into
+// LDS (no VGPR staging), three slabs ahead of the MFMAs; out-of-range rows or K read as zeros
+// through the buffer's range check. Within a row the four 16-byte chunks are XOR-swizzled by
+// ((row >> 1) & 3), so a wave's ds_read_b128 of 32 rows at one k hits distinct banks in every
+// 8-lane group. Each slab is two 16-wide k-steps; the workgroup barrier sits between them, so
+// the next slab's first fragments are read while the current slab's second k-step runs.
+// Epilogues: each wave stages its 128 x 128 tile of round_T(C) in LDS, then walks token rows
+// with 16 lanes x 16 bytes per row, so every hidden load and output store is a coalesced
+// 256-byte row segment. The key pass reduces its three sums per row across the 16 lanes with
+// DPP row shifts and combines the two column waves in LDS. Workgroup ids are remapped so the
+// 32 CUs of one XCD work on a compact group of tiles (8 token tiles x 4 column tiles) and share
+// their operands in that XCD's L2.
 #include "me_common.h"
+
+#include <type_traits>
 
 namespace me {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int int32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kTile = 256;         // output tile edge (j and n)
-constexpr int kRowBytes = 128;     // bytes of K per row per k-step
-constexpr int kOperandBytes = kTile * kRowBytes;            // 32 KiB
-constexpr int kStagePitch = 512 + 16;                       // epilogue row: 512 B + pad
-constexpr int kStageBytes = kTile * kStagePitch;            // 132 KiB
-constexpr int kLoopBytes = 4 * kOperandBytes;               // 2 buffers x (A + B) = 128 KiB
-constexpr int kSmemBytes = kStageBytes > kLoopBytes ? kStageBytes : kLoopBytes;
-constexpr int kGroupTiles = 8;     // token tiles per XCD group
+constexpr int kTile = 256;                         // output tile edge (j and n)
+constexpr int kSlab = 64;                          // bytes of K per row per ring slot
+constexpr int kStages = 5;                         // ring slots (3 slabs in flight)
+constexpr int kOperandStage = kTile * kSlab;       // 16 KiB
+constexpr int kStageBytes = 2 * kOperandStage;     // A (W rows) + B (mem rows)
+constexpr int kRingBytes = kStages * kStageBytes;  // 160 KiB
+constexpr int kDmaPerOperand = kOperandStage / (kThreads * 16);  // 16-byte loads per thread
+constexpr int kStagePitch = 256 + 8;               // epilogue staging row: 256 B + pad
+constexpr int kWaveStage = 128 * kStagePitch;      // one wave's staged 128-row tile
+constexpr int kGroupTiles = 8;                     // token tiles per XCD group
 constexpr int kXcds = 8;
+constexpr uint32_t kBufferConfig = 0x00020000u;    // raw buffer descriptor word 3 (gfx9 family)
+static_assert(4 * kWaveStage + 2 * kTile * 3 * 4 <= kRingBytes, "epilogue must fit in the ring");
 
 enum Phase : int { kKey = 0, kValue = 1 };
 
@@ -59,6 +73,7 @@ struct GateArgs {
     float *partials;        // [n_jt][n][3] per-column-tile sums (sum K^2, sum x qs ks K, sum x^2)
     float *alpha_eff;       // [n] gate of each token, 0 where keep is false
     int64_t n, d, m;
+    uint32_t mem_bytes, w_bytes;  // buffer ranges (reads past them return zeros)
     int scale_bf16;
     int sqrt_mode;
     int n_jt, n_nt, total_tiles, per_xcd;
@@ -84,127 +99,111 @@ __device__ __forceinline__ uint16_t from_f<uint16_t>(float v) { return float_to_
 template <typename T>
 __device__ __forceinline__ float round_t(float v) { return to_f<T>(from_f<T>(v)); }
 
-__device__ __forceinline__ float load_scale(const void *p, int is_bf16, int64_t j) {
-    return is_bf16 ? bf16_bits_to_float(static_cast<const uint16_t *>(p)[j])
-                   : static_cast<const float *>(p)[j];
-}
-
-// Loads/stores E consecutive elements of type X as floats (E * sizeof(X) is 8, 16 or 32 bytes).
+// E consecutive elements of X (E * sizeof(X) a multiple of 8 bytes, 8-byte aligned) as floats.
 template <typename X, int E>
-__device__ __forceinline__ void load_row(const uint8_t *p, float (&v)[E]) {
-    constexpr int kBytes = E * sizeof(X);
-    static_assert(kBytes % 8 == 0, "row chunk must be a multiple of 8 bytes");
-    uint32_t w[kBytes / 4];
+__device__ __forceinline__ void load_run(const uint8_t *p, float (&v)[E]) {
+    constexpr int kWords = E * sizeof(X) / 4;
+    uint32_t w[kWords];
 #pragma unroll
-    for (int q = 0; q < kBytes / 16; ++q) {
-        const uint4 u = reinterpret_cast<const uint4 *>(p)[q];
-        w[4 * q] = u.x; w[4 * q + 1] = u.y; w[4 * q + 2] = u.z; w[4 * q + 3] = u.w;
-    }
-    if (kBytes % 16 == 8) {
-        const uint2 u = reinterpret_cast<const uint2 *>(p)[kBytes / 8 - 1];
-        w[kBytes / 4 - 2] = u.x; w[kBytes / 4 - 1] = u.y;
+    for (int q = 0; q < kWords; q += 2) {
+        const uint2 u = reinterpret_cast<const uint2 *>(p)[q / 2];
+        w[q] = u.x;
+        w[q + 1] = u.y;
     }
     const X *x = reinterpret_cast<const X *>(w);
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = to_f<X>(x[e]);
 }
 
-template <typename X, int E>
-__device__ __forceinline__ void store_row(uint8_t *p, const float (&v)[E]) {
-    constexpr int kBytes = E * sizeof(X);
-    uint32_t w[kBytes / 4];
-    X *x = reinterpret_cast<X *>(w);
-#pragma unroll
-    for (int e = 0; e < E; ++e) x[e] = from_f<X>(v[e]);
-#pragma unroll
-    for (int q = 0; q < kBytes / 16; ++q)
-        reinterpret_cast<uint4 *>(p)[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
-    if (kBytes % 16 == 8)
-        reinterpret_cast<uint2 *>(p)[kBytes / 8 - 1] = make_uint2(w[kBytes / 4 - 2], w[kBytes / 4 - 1]);
+// ---- memory -> LDS without registers ---------------------------------------------------------
+__device__ __forceinline__ int32x4 buffer_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    int32x4 r;
+    r.x = static_cast<int>(static_cast<uint32_t>(a));
+    r.y = static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xffffu);  // stride 0
+    r.z = static_cast<int>(bytes);
+    r.w = static_cast<int>(kBufferConfig);
+    return r;
 }
 
-// Raw bytes of E elements of X, loaded now and unpacked later (keeps a batch of global loads
-// in flight without converting them to floats first).
-template <typename X, int E>
-struct RawRow {
-    static constexpr int kWords = E * sizeof(X) / 4;
-    uint32_t w[kWords];
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)p));
+}
+
+// One wave moves 64 x 16 bytes: lane l's chunk at byte `voffset` of the buffer lands at LDS
+// address lds_base + 16 * l. A voffset at or past the buffer's range reads zeros. The load is
+// counted by vmcnt; the caller waits for it explicitly (the compiler does not see it).
+__device__ __forceinline__ void dma16(const int32x4 &rsrc, uint32_t lds_base, uint32_t voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voffset), "s"(rsrc)
+                 : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// ---- MFMA k-steps ----------------------------------------------------------------------------
+// A slot holds swizzled [256 rows][64 B] tiles of A and B; a slab is two 16-wide (bf16) k-steps.
+// The wave's A rows are wj*128 + [0,128), its B rows wn*128 + [0,128). For k-step ks, lane l
+// reads row (l & 31) of each 32-row subtile at logical chunk 2*ks + (l >> 5): lanes 0-31 carry
+// one half of the step's k values and lanes 32-63 the other, identically for A and B, which is
+// all the dot product needs.
+template <typename T>
+struct Frag;
+template <>
+struct Frag<uint16_t> {
+    bf16x8 a[4], b[4];
+};
+template <>
+struct Frag<float> {
+    float4 a[4], b[4];
 };
 
-template <typename X, int E>
-__device__ __forceinline__ void load_raw(const uint8_t *p, RawRow<X, E> &r) {
-    constexpr int kBytes = E * sizeof(X);
-#pragma unroll
-    for (int q = 0; q < kBytes / 16; ++q) {
-        const uint4 u = reinterpret_cast<const uint4 *>(p)[q];
-        r.w[4 * q] = u.x; r.w[4 * q + 1] = u.y; r.w[4 * q + 2] = u.z; r.w[4 * q + 3] = u.w;
-    }
-    if (kBytes % 16 == 8) {
-        const uint2 u = reinterpret_cast<const uint2 *>(p)[kBytes / 8 - 1];
-        r.w[kBytes / 4 - 2] = u.x; r.w[kBytes / 4 - 1] = u.y;
-    }
-}
-
-template <typename X, int E>
-__device__ __forceinline__ void unpack(const RawRow<X, E> &r, float (&v)[E]) {
-    const X *x = reinterpret_cast<const X *>(r.w);
-#pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = to_f<X>(x[e]);
-}
-
-// ---- MFMA step over one 128-byte k-slab ---------------------------------------------------
-// As/Bs: swizzled [256 rows][128 B] tiles. The wave's A rows are wj*128 + [0,128), its B rows
-// wn*128 + [0,128). Lane l reads row (l & 31) of each 32-row subtile at 16-byte chunk
-// c = 2*ks + (l >> 5), so lanes 0-31 carry one half of the step's k values and lanes 32-63 the
-// other; A and B use the same assignment, which is all the dot product needs.
 template <typename T>
-__device__ __forceinline__ void mfma_slab(const uint8_t *As, const uint8_t *Bs, int wj, int wn,
-                                          int lane, floatx16 (&acc)[4][4]);
-
-template <>
-__device__ __forceinline__ void mfma_slab<uint16_t>(const uint8_t *As, const uint8_t *Bs, int wj,
-                                                    int wn, int lane, floatx16 (&acc)[4][4]) {
-    const int r = lane & 31, swz = lane & 7;
+__device__ __forceinline__ void load_frag(const uint8_t *slot, int ks, int wj, int wn, int lane,
+                                          Frag<T> &f) {
+    const int r = lane & 31;
+    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 3)) << 4;
+    using V = decltype(f.a[0]);
+    using VV = typename std::remove_reference<V>::type;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        const int c = ((2 * ks + (lane >> 5)) ^ swz) << 4;
-        bf16x8 af[4], bf[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            af[s] = *reinterpret_cast<const bf16x8 *>(As + (wj * 128 + s * 32 + r) * kRowBytes + c);
-            bf[s] = *reinterpret_cast<const bf16x8 *>(Bs + (wn * 128 + s * 32 + r) * kRowBytes + c);
-        }
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bf[b], acc[a][b], 0, 0, 0);
+    for (int s = 0; s < 4; ++s) {
+        f.a[s] = *reinterpret_cast<const VV *>(slot + (wj * 128 + s * 32 + r) * kSlab + c);
+        f.b[s] = *reinterpret_cast<const VV *>(slot + kOperandStage + (wn * 128 + s * 32 + r) * kSlab + c);
     }
 }
 
-template <>
-__device__ __forceinline__ void mfma_slab<float>(const uint8_t *As, const uint8_t *Bs, int wj,
-                                                 int wn, int lane, floatx16 (&acc)[4][4]) {
-    const int r = lane & 31, swz = lane & 7;
+__device__ __forceinline__ void mfma_step(const Frag<uint16_t> &f, floatx16 (&acc)[4][4]) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        const int c = ((2 * ks + (lane >> 5)) ^ swz) << 4;
-        float4 af[4], bf[4];
+    for (int x = 0; x < 4; ++x)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            af[s] = *reinterpret_cast<const float4 *>(As + (wj * 128 + s * 32 + r) * kRowBytes + c);
-            bf[s] = *reinterpret_cast<const float4 *>(Bs + (wn * 128 + s * 32 + r) * kRowBytes + c);
+        for (int y = 0; y < 4; ++y)
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x], f.b[y], acc[x][y], 0, 0, 0);
+}
+
+__device__ __forceinline__ void mfma_step(const Frag<float> &f, floatx16 (&acc)[4][4]) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].x, f.b[y].x, acc[x][y], 0, 0, 0);
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].y, f.b[y].y, acc[x][y], 0, 0, 0);
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].z, f.b[y].z, acc[x][y], 0, 0, 0);
+            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].w, f.b[y].w, acc[x][y], 0, 0, 0);
         }
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].x, bf[b].x, acc[a][b], 0, 0, 0);
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].y, bf[b].y, acc[a][b], 0, 0, 0);
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].z, bf[b].z, acc[a][b], 0, 0, 0);
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].w, bf[b].w, acc[a][b], 0, 0, 0);
-            }
-    }
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16i .. 16i+15), exact in lane 16i + 15: an inclusive
+// scan by row shifts of 1, 2, 4 and 8 (out-of-row sources read as 0).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, true));
+    return v;
 }
 
 __device__ __forceinline__ float gate_alpha(float sx2, float sk2, float sck, const GateArgs &a) {
@@ -221,9 +220,7 @@ __device__ __forceinline__ float gate_alpha(float sx2, float sk2, float sck, con
 
 template <typename T, typename H, int PHASE>
 __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[kSmemBytes];
-    __shared__ float s_alpha[kTile];
-    __shared__ float s_part[kTile][3];
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kRingBytes];
 
     // ---- tile of this workgroup: XCD-compact groups of 8 token tiles x all column tiles
     const int bid = blockIdx.x;
@@ -242,17 +239,55 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wj = wave >> 1, wn = wave & 1;
 
-    // the value pass reads the tile's gates now and parks them in LDS after the K loop
+    // the value pass reads its tokens' gates now; they are parked in LDS after the K loop
     float alpha_reg = 0.f;
-    if (PHASE == kValue) {
-        if (n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
-    } else {
-        s_part[tid][0] = 0.f;
-        s_part[tid][1] = 0.f;
-        s_part[tid][2] = 0.f;
-    }
+    if (PHASE == kValue && n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
 
-    // ---- GEMM: acc[a][b] = W[j-subtile a] x mem[n-subtile b]^T over the full K
+    // ---- K loop over a 5-slot ring of 64-byte slabs
+    const uint32_t row_bytes = static_cast<uint32_t>(a.m * sizeof(T));
+    const int slabs = static_cast<int>(ceil_div(row_bytes, kSlab));
+    const int32x4 rsrc_w = buffer_rsrc(a.w, a.w_bytes);
+    const int32x4 rsrc_m = buffer_rsrc(a.mem, a.mem_bytes);
+    // lane l of LDS segment s (16 rows) fills row 16 s + l / 4, physical chunk l % 4, which holds
+    // the logical chunk (l % 4) ^ ((row >> 1) & 3) of the row's slab
+    const uint32_t chunk = static_cast<uint32_t>((lane & 3) ^ ((lane >> 3) & 3)) * 16u;
+    uint32_t offw[kDmaPerOperand], offm[kDmaPerOperand];
+    bool okw[kDmaPerOperand], okm[kDmaPerOperand];
+#pragma unroll
+    for (int i = 0; i < kDmaPerOperand; ++i) {
+        const int row = (wave * kDmaPerOperand + i) * 16 + (lane >> 2);
+        okw[i] = j0 + row < a.d;
+        okm[i] = n0 + row < a.n;
+        offw[i] = okw[i] ? static_cast<uint32_t>(j0 + row) * row_bytes + chunk : 0u;
+        offm[i] = okm[i] ? static_cast<uint32_t>(n0 + row) * row_bytes + chunk : 0u;
+    }
+    const uint32_t ring_lds = lds_addr(ring);
+    auto issue = [&](int kt) {
+        const uint32_t kb = static_cast<uint32_t>(kt) * kSlab;
+        const bool kin = kb + chunk < row_bytes;
+        const uint32_t slot = ring_lds + static_cast<uint32_t>(kt % kStages) * kStageBytes;
+#pragma unroll
+        for (int i = 0; i < kDmaPerOperand; ++i) {
+            const uint32_t seg = static_cast<uint32_t>(wave * kDmaPerOperand + i) * 1024u;
+            dma16(rsrc_w, __builtin_amdgcn_readfirstlane(slot + seg),
+                  okw[i] && kin ? offw[i] + kb : a.w_bytes);
+            dma16(rsrc_m, __builtin_amdgcn_readfirstlane(slot + kOperandStage + seg),
+                  okm[i] && kin ? offm[i] + kb : a.mem_bytes);
+        }
+    };
+    // wait until at most `later` slabs issued after the awaited one are still in flight
+    auto wait_slab = [&](int later) {
+        constexpr int kLoads = 2 * kDmaPerOperand;  // vmcnt of one slab
+        if (later >= 3)
+            wait_vmcnt<3 * kLoads>();
+        else if (later == 2)
+            wait_vmcnt<2 * kLoads>();
+        else if (later == 1)
+            wait_vmcnt<kLoads>();
+        else
+            wait_vmcnt<0>();
+    };
+
     floatx16 acc[4][4];
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -261,152 +296,162 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.f;
 
-    constexpr int kElems = kRowBytes / sizeof(T);  // k values per row per step
-    const int64_t row_bytes = a.m * static_cast<int64_t>(sizeof(T));
-    const int ksteps = static_cast<int>(ceil_div(a.m, kElems));
-    uint4 ra[8], rb[8];
-
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int q = tid + kThreads * i;
-            const int row = q >> 3, c = q & 7;
-            const int64_t kb = static_cast<int64_t>(kt) * kRowBytes + c * 16;  // byte offset in K
-            const bool kin = kb < row_bytes;
-            ra[i] = (kin && j0 + row < a.d)
-                        ? *reinterpret_cast<const uint4 *>(a.w + (j0 + row) * row_bytes + kb)
-                        : make_uint4(0, 0, 0, 0);
-            rb[i] = (kin && n0 + row < a.n)
-                        ? *reinterpret_cast<const uint4 *>(a.mem + (n0 + row) * row_bytes + kb)
-                        : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto sstore = [&](int buf) {
-        uint8_t *As = smem + buf * 2 * kOperandBytes;
-        uint8_t *Bs = As + kOperandBytes;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int q = tid + kThreads * i;
-            const int row = q >> 3, c = q & 7;
-            const int off = row * kRowBytes + ((c ^ (row & 7)) << 4);
-            *reinterpret_cast<uint4 *>(As + off) = ra[i];
-            *reinterpret_cast<uint4 *>(Bs + off) = rb[i];
-        }
-    };
-
-    gload(0);
-    sstore(0);
+    for (int kt = 0; kt < min(slabs, kStages - 1); ++kt) issue(kt);
+    wait_slab(min(slabs - 1, kStages - 2));
     __syncthreads();
-    for (int kt = 0; kt < ksteps; ++kt) {
-        if (kt + 1 < ksteps) gload(kt + 1);
-        const uint8_t *As = smem + (kt & 1) * 2 * kOperandBytes;
-        mfma_slab<T>(As, As + kOperandBytes, wj, wn, lane, acc);
-        if (kt + 1 < ksteps) sstore((kt + 1) & 1);
-        __syncthreads();
+    Frag<T> f0, f1;
+    load_frag<T>(ring, 0, wj, wn, lane, f0);
+    for (int kt = 0; kt < slabs; ++kt) {
+        const uint8_t *slot = ring + (kt % kStages) * kStageBytes;
+        load_frag<T>(slot, 1, wj, wn, lane, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step(f0, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 1 < slabs) {
+            wait_slab(min(slabs - 2 - kt, kStages - 3));
+            __syncthreads();  // slab kt+1 is in LDS; every wave is done reading slab kt-1
+            if (kt + kStages - 1 < slabs) issue(kt + kStages - 1);
+            load_frag<T>(ring + ((kt + 1) % kStages) * kStageBytes, 0, wj, wn, lane, f0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step(f1, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // the ring is free for the epilogue
+
+    // ---- epilogue: each wave stages round_T of its 128 x 128 tile as [token][column] rows
+    // (pitch kStagePitch), then walks its token rows with 16 lanes x 16 bytes per row. fp32
+    // tiles go in two column halves of 64.
+    constexpr int kPasses = sizeof(T) == 2 ? 1 : 2;
+    constexpr int kPassCols = 128 / kPasses;     // columns staged per pass
+    constexpr int kLaneCols = 16 / sizeof(T);    // columns per lane in the row walk (8 / 4)
+    constexpr int kRowWords = kLaneCols * sizeof(H) / 4;  // hidden words per lane per row
+    constexpr int kBatch = kRowWords <= 4 ? 32 : 16;      // rows whose hidden loads are in flight
+    uint8_t *stage = ring + wave * kWaveStage;
+    float *s_aux = reinterpret_cast<float *>(ring + 4 * kWaveStage);  // [2][256][3] or [256]
+    const int r = lane & 31, half = lane >> 5;
+    const int l16 = lane & 15, rsub = lane >> 4;  // row walk: lane column block, row in 4
+    const int64_t ntok0 = n0 + wn * 128;          // first token of the wave
+
+    if (PHASE == kValue) {
+        s_aux[tid] = alpha_reg;
+    } else {
+        for (int e = tid; e < 2 * kTile * 3; e += kThreads) s_aux[e] = 0.f;
     }
 
-    if (PHASE == kValue) s_alpha[tid] = alpha_reg;  // read after the staging barrier
-
-    // ---- epilogue: stage round_T(C) as [token][column] rows in LDS, then walk token rows
-    constexpr int kPasses = sizeof(T) == 2 ? 1 : 2;     // fp32 tiles are staged in two halves
-    constexpr int kPassCols = kTile / kPasses;          // columns per pass
-    constexpr int kLaneCols = kPassCols / 32;           // columns per lane (8 bf16 / 4 fp32)
-    const int half = lane >> 5, sub = lane & 31;
-
     for (int pass = 0; pass < kPasses; ++pass) {
-        if (kPasses == 1 || wj == pass) {
+        // stage: acc[x][y][4g + e] is token 32y + r, column 32x + 8g + 4*half + e
 #pragma unroll
-            for (int x = 0; x < 4; ++x)
+        for (int x = 0; x < 4; ++x) {
+            if (kPasses == 2 && (x >> 1) != pass) continue;
 #pragma unroll
-                for (int y = 0; y < 4; ++y) {
-                    const int nl = wn * 128 + y * 32 + sub;
+            for (int y = 0; y < 4; ++y)
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        // rows 8g + 4*half + [0,4) of the 32x32 MFMA output are 4 consecutive j
-                        const int jl = (kPasses == 1 ? wj * 128 : 0) + x * 32 + 8 * g + 4 * half;
-                        float v[4] = {acc[x][y][4 * g], acc[x][y][4 * g + 1], acc[x][y][4 * g + 2],
-                                      acc[x][y][4 * g + 3]};
-                        store_row<T, 4>(smem + nl * kStagePitch + jl * sizeof(T), v);
-                    }
+                for (int g = 0; g < 4; ++g) {
+                    const int col = (x % (4 / kPasses)) * 32 + 8 * g + 4 * half;
+                    uint32_t w[sizeof(T)];
+                    T *tv = reinterpret_cast<T *>(w);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) tv[e] = from_f<T>(acc[x][y][4 * g + e]);
+                    uint8_t *p = stage + (y * 32 + r) * kStagePitch + col * sizeof(T);
+                    reinterpret_cast<uint2 *>(p)[0] = make_uint2(w[0], w[1]);
+                    if (sizeof(T) == 4) reinterpret_cast<uint2 *>(p)[1] = make_uint2(w[2], w[3]);
                 }
         }
-        __syncthreads();
+        __syncthreads();  // staging (and s_aux) visible
 
-        // walk token rows: a half-wave (32 lanes x kLaneCols columns) per row, 8 rows per
-        // step across the workgroup; the hidden loads of a whole batch of rows are issued
-        // before any of them is used
-        constexpr int kIters = kTile / 8;
-        constexpr int kHBytes = kLaneCols * sizeof(H);
-        constexpr int kBatch = kHBytes <= 16 ? kIters : kIters / 2;
-        const int jl = sub * kLaneCols;
-        const int64_t j = j0 + pass * kPassCols + jl;
-        const bool jlive = j < a.d;
-        float w[kLaneCols];  // q_scale * k_scale of the lane's columns (key pass)
+        const int64_t jl = j0 + wj * 128 + pass * kPassCols + l16 * kLaneCols;  // lane's first column
+        const bool jok = jl < a.d;  // d is a multiple of 8: a lane's columns are all in or all out
+        float wcol[kLaneCols];  // q_scale * k_scale of the lane's columns (key pass)
 #pragma unroll
-        for (int e = 0; e < kLaneCols; ++e) {
-            w[e] = 1.f;
-            if (PHASE == kKey && jlive && a.q_delta != nullptr)
-                w[e] = (1.f + load_scale(a.q_delta, a.scale_bf16, j + e)) *
-                       (1.f + load_scale(a.k_delta, a.scale_bf16, j + e));
+        for (int e = 0; e < kLaneCols; ++e) wcol[e] = 1.f;
+        if (PHASE == kKey && jok && a.q_delta != nullptr) {
+            float qv[kLaneCols], kv[kLaneCols];
+            if (a.scale_bf16) {
+                load_run<uint16_t, kLaneCols>(static_cast<const uint8_t *>(a.q_delta) + jl * 2, qv);
+                load_run<uint16_t, kLaneCols>(static_cast<const uint8_t *>(a.k_delta) + jl * 2, kv);
+            } else {
+                load_run<float, kLaneCols>(static_cast<const uint8_t *>(a.q_delta) + jl * 4, qv);
+                load_run<float, kLaneCols>(static_cast<const uint8_t *>(a.k_delta) + jl * 4, kv);
+            }
+#pragma unroll
+            for (int e = 0; e < kLaneCols; ++e) wcol[e] = (1.f + qv[e]) * (1.f + kv[e]);
         }
-        for (int b0 = 0; b0 < kIters; b0 += kBatch) {
-            RawRow<H, kLaneCols> raw[kBatch];
+        for (int b0 = 0; b0 < 32; b0 += kBatch) {
+            uint32_t xr[kBatch][kRowWords];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                const int64_t n = n0 + (b0 + u) * 8 + wave * 2 + half;
-                if (jlive && n < a.n) {
-                    load_raw<H, kLaneCols>(a.hidden + (n * a.d + j) * sizeof(H), raw[u]);
+                const int row = (b0 + u) * 4 + rsub;
+                const int64_t n = ntok0 + row;
+                if (jok && n < a.n) {
+                    const uint8_t *p = a.hidden + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
+#pragma unroll
+                    for (int q = 0; q < kRowWords; q += 2) {
+                        const uint2 v = reinterpret_cast<const uint2 *>(p)[q / 2];
+                        xr[u][q] = v.x;
+                        xr[u][q + 1] = v.y;
+                    }
                 } else {
 #pragma unroll
-                    for (int q = 0; q < RawRow<H, kLaneCols>::kWords; ++q) raw[u].w[q] = 0u;
+                    for (int q = 0; q < kRowWords; ++q) xr[u][q] = 0u;
                 }
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                const int nl = (b0 + u) * 8 + wave * 2 + half;
-                const int64_t n = n0 + nl;
-                const bool live = jlive && n < a.n;
-                float c[kLaneCols], x[kLaneCols];
-                load_row<T, kLaneCols>(smem + nl * kStagePitch + jl * sizeof(T), c);
-                unpack<H, kLaneCols>(raw[u], x);
+                const int row = (b0 + u) * 4 + rsub;
+                const int64_t n = ntok0 + row;
+                const uint8_t *sp = stage + row * kStagePitch + (l16 * kLaneCols) * sizeof(T);
+                uint32_t cw[4];
+                const uint2 c0 = reinterpret_cast<const uint2 *>(sp)[0];
+                const uint2 c1 = reinterpret_cast<const uint2 *>(sp)[1];
+                cw[0] = c0.x; cw[1] = c0.y; cw[2] = c1.x; cw[3] = c1.y;
+                const T *cv = reinterpret_cast<const T *>(cw);
+                const H *xv = reinterpret_cast<const H *>(xr[u]);
                 if (PHASE == kKey) {
                     float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
 #pragma unroll
                     for (int e = 0; e < kLaneCols; ++e) {
-                        sk2 += c[e] * c[e];
-                        sck += x[e] * w[e] * c[e];
-                        sx2 += x[e] * x[e];
+                        const float kv = to_f<T>(cv[e]);
+                        const float x = to_f<H>(xv[e]);
+                        sk2 += kv * kv;
+                        sck += x * wcol[e] * kv;
+                        sx2 += x * x;
                     }
+                    sk2 = row16_sum(sk2);
+                    sck = row16_sum(sck);
+                    sx2 = row16_sum(sx2);
+                    if (l16 == 15) {
+                        float *p = s_aux + (wj * kTile + wn * 128 + row) * 3;
+                        p[0] += sk2;
+                        p[1] += sck;
+                        p[2] += sx2;
+                    }
+                } else if (jok && n < a.n) {
+                    const float alpha = s_aux[wn * 128 + row];
+                    uint32_t ow[kRowWords];
+                    H *ov = reinterpret_cast<H *>(ow);
 #pragma unroll
-                    for (int off = 16; off >= 1; off >>= 1) {
-                        sk2 += __shfl_xor(sk2, off, 32);
-                        sck += __shfl_xor(sck, off, 32);
-                        sx2 += __shfl_xor(sx2, off, 32);
-                    }
-                    if (sub == 0) {
-                        s_part[nl][0] += sk2;
-                        s_part[nl][1] += sck;
-                        s_part[nl][2] += sx2;
-                    }
-                } else if (live) {
-                    const float alpha = s_alpha[nl];
-                    float o[kLaneCols];
+                    for (int e = 0; e < kLaneCols; ++e)
+                        ov[e] = from_f<H>(to_f<H>(xv[e]) + round_t<H>(alpha * to_f<T>(cv[e])));
+                    uint8_t *p = a.out + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
 #pragma unroll
-                    for (int e = 0; e < kLaneCols; ++e) o[e] = x[e] + round_t<H>(alpha * c[e]);
-                    store_row<H, kLaneCols>(a.out + (n * a.d + j) * sizeof(H), o);
+                    for (int q = 0; q < kRowWords; q += 2)
+                        reinterpret_cast<uint2 *>(p)[q / 2] = make_uint2(ow[q], ow[q + 1]);
                 }
             }
         }
-        __syncthreads();
+        __syncthreads();  // the staging area is reused by the next pass; s_aux is complete
     }
 
     if (PHASE == kKey) {
         const int64_t n = n0 + tid;
         if (n < a.n) {
-            float *p = a.partials + (static_cast<int64_t>(jt) * a.n + n) * 3;
-            p[0] = s_part[tid][0];
-            p[1] = s_part[tid][1];
-            p[2] = s_part[tid][2];
+            const float *p0 = s_aux + tid * 3;
+            const float *p1 = s_aux + (kTile + tid) * 3;
+            float *o = a.partials + (static_cast<int64_t>(jt) * a.n + n) * 3;
+            o[0] = p0[0] + p1[0];
+            o[1] = p0[1] + p1[1];
+            o[2] = p0[2] + p1[2];
         }
     }
 }
@@ -464,16 +509,20 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
                  "shape too large");
     if (n == 0) return ME_OK;
     ME_CHECK_ARG(hidden && mem && w_key && w_value && out, "null tensor pointer");
-    const size_t esz = dtype_size(dtype), hsz = dtype_size(hidden_dtype);
+    const size_t esz = dtype_size(dtype);
     ME_CHECK_ARG((mem_dim * esz) % 16 == 0, "mem_dim * element size must be a multiple of 16 bytes");
     ME_CHECK_ARG(model_dim % 8 == 0, "model_dim must be a multiple of 8");
+    ME_CHECK_ARG(n * mem_dim * static_cast<int64_t>(esz) < (int64_t{1} << 31) &&
+                     model_dim * mem_dim * static_cast<int64_t>(esz) < (int64_t{1} << 31),
+                 "mem and the projection weights must each be under 2 GiB");
     ME_CHECK_ARG(aligned16(hidden) && aligned16(mem) && aligned16(w_key) && aligned16(w_value) &&
                      aligned16(out),
                  "tensors must be 16-byte aligned");
-    (void)hsz;
     if (gate_mode == ME_GATE_SCALAR_SQRT) {
         ME_CHECK_ARG(q_scale_delta && k_scale_delta, "scalar_sqrt needs q/k scale deltas");
         ME_CHECK_ARG(scale_dtype == ME_BF16 || scale_dtype == ME_F32, "scale dtype must be bf16/fp32");
+        ME_CHECK_ARG(aligned16(q_scale_delta) && aligned16(k_scale_delta),
+                     "scale tensors must be 16-byte aligned");
     }
     const size_t need = workspace_bytes(n, model_dim);
     if (workspace == nullptr || workspace_size < need) {
@@ -496,6 +545,8 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     a.n = n;
     a.d = model_dim;
     a.m = mem_dim;
+    a.mem_bytes = static_cast<uint32_t>(n * mem_dim * esz);
+    a.w_bytes = static_cast<uint32_t>(model_dim * mem_dim * esz);
     a.n_jt = static_cast<int>(ceil_div(model_dim, kTile));
     a.n_nt = static_cast<int>(ceil_div(n, kTile));
     a.total_tiles = a.n_jt * a.n_nt;

@@ -46,16 +46,14 @@ inline size_t dtype_size(int dt) {
 
 // ---------------------------------------------------------------------------------------------
 // bf16 <-> fp32. bf16 is the upper half of an fp32; fp32 -> bf16 rounds to nearest, ties to
-// even (what torch's .to(torch.bfloat16) does), NaN stays a quiet NaN.
+// even (what torch's .to(torch.bfloat16) does), NaN stays NaN. gfx950 converts in hardware
+// (v_cvt_pk_bf16_f32, two values per instruction).
 __device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
 __device__ __forceinline__ uint16_t float_to_bf16_bits_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // Value of an fp32 after a round trip through bf16 (the rounding a bf16 tensor applies).

@@ -193,3 +193,25 @@ def test_gemma_prefill_forward_sampled():
     assert_close_out(got, ref, h, torch.bfloat16)
     del eng
     torch.cuda.empty_cache()
+
+
+def test_projection_rounds_to_nearest_even():
+    # hidden = 0 makes the scalar gate exactly 0.5 (s = 0), so out = 0.5 * bf16(W_V e) exactly:
+    # the projection's fp32 -> bf16 rounding is observed directly, ties included
+    d, M = 64, 16
+    k = torch.arange(d, dtype=torch.float32) - 32           # t = k / 512: every rounding case
+    t = (k / 512).to(torch.bfloat16)
+    wv = torch.zeros(d, M, dtype=torch.bfloat16)
+    wv[:, 0] = torch.where(k >= 0, 1.0, -1.0).to(torch.bfloat16)
+    wv[:, 1] = t
+    mem = torch.zeros(4, M, dtype=torch.bfloat16)
+    mem[:, 0] = 1.0
+    mem[:, 1] = 1.0
+    hidden = torch.zeros(4, d, dtype=torch.bfloat16)
+    wk = torch.ones(d, M, dtype=torch.bfloat16)
+    with torch.no_grad():
+        out, alpha = ops.gate_residual(hidden.to(DEV), mem.to(DEV), wk.to(DEV), wv.to(DEV), None, None,
+                                       0, None, True)
+    assert torch.equal(alpha.cpu(), torch.full((4,), 0.5))
+    want = (wv[:, 0].float() + t.float()).to(torch.bfloat16)  # fp32 sum is exact; RNE to bf16
+    assert torch.equal((out.cpu().float() * 2).to(torch.bfloat16), want.expand(4, d))
