@@ -161,6 +161,73 @@ int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n, int64_t mo
                      int scale_dtype, int gate_mode, const uint8_t *keep, void *out,
                      float *alpha_out, void *workspace, size_t workspace_size, void *stream);
 
+/*
+ * me_dedup_workspace_size -- bytes of workspace me_dedup needs for n keys.
+ */
+int me_dedup_workspace_size(int64_t n, size_t *bytes);
+
+/*
+ * me_dedup -- touched-row dedup with coalesced gradients.
+ * Replaces torch.unique(flat, return_inverse=True) and zeros(n_uniq, D).index_add_(0, inv, g)
+ * (micro_engram/rows.py:81, 117-118; add_sparse_grad rows.py:137-147).
+ *
+ *   keys       int64 [n], every key in [0, key_bound) (table offset + row)
+ *   grads      nullable [n, dim] of grad_dtype (ME_F32 / ME_BF16): the gradient row of each key
+ *   uniq       int64 [n]: the count unique keys, ascending, in uniq[0 .. count)
+ *   inv        int64 [n]: uniq[inv[i]] == keys[i]
+ *   gsum       fp32 [n, dim] (needed when grads is given): row u = fp32 sum of the grads of the
+ *              keys equal to uniq[u], added in increasing i from +0.0 (bit-exact with CPU
+ *              index_add_)
+ *   count      int64 [1], device: the number of unique keys
+ */
+int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const void *grads, int grad_dtype,
+             int32_t dim, int64_t *uniq, int64_t *inv, float *gsum, int64_t *count,
+             void *workspace, size_t workspace_size, void *stream);
+
+/*
+ * me_sumsq -- sum of squares of n fp32 values into *out (or added to it when accumulate != 0),
+ * in a fixed order. The squared gradient norm of RowTables.clip (micro_engram/rows.py:214-223).
+ * workspace: at least 1 KiB.
+ */
+int me_sumsq(const float *x, int64_t n, float *out, int accumulate, void *workspace,
+             size_t workspace_size, void *stream);
+
+/*
+ * me_sparse_adam -- one LazyAdamW step on the given rows of n_tables tables.
+ * Replaces the row branches of LazyAdamW.step (micro_engram/optim.py:65-133): with lazy != 0,
+ * rows whose gradient is all zero are skipped (optim.py:88-104); weight decay, first moment, second moment (one
+ * fp32 value per row when rowwise != 0, else per value in sq_dtype), bias correction with each
+ * table's own step count, and write-back of weights and moments, with stochastic rounding to bf16
+ * when stochastic_rounding != 0 (optim.py:33-44).
+ *
+ *   HOST arrays [n_tables]: params, exp_avgs (device [rows_k, dim], param_dtype), exp_avg_sqs
+ *   (device [rows_k] fp32 or [rows_k, dim] sq_dtype), rows (device int64 [n_rows_k], unique),
+ *   grads (device fp32 [n_rows_k, dim]), n_rows, steps (the step count after this step's
+ *   increment), stream_ids (< 65536, distinct per table: selects the table's rounding noise)
+ *   grad_sumsq   nullable device fp32 scalar: gradients are scaled by
+ *                min(max_norm / (sqrt(*grad_sumsq) + 1e-6), 1) first (RowTables.clip,
+ *                rows.py:224-231)
+ * The rounding noise of element (row, col) is 16 bits of Philox4x32-10 keyed by seed with counter
+ * (row low, row high, step, stream_id << 16 | which << 14 | col >> 3), word (col >> 1) & 3,
+ * half col & 1; which = 0 weights, 1 first moment, 2 per-value second moment.
+ */
+int me_sparse_adam(int32_t n_tables, void *const *params, void *const *exp_avgs,
+                   void *const *exp_avg_sqs, const int64_t *const *rows, const float *const *grads,
+                   const int64_t *n_rows, const int64_t *steps, const int32_t *stream_ids,
+                   int32_t dim, int param_dtype, int rowwise, int sq_dtype, int lazy, double lr,
+                   double beta1, double beta2, double eps, double weight_decay,
+                   int stochastic_rounding, uint64_t seed, const float *grad_sumsq,
+                   double max_norm, void *stream);
+
+/*
+ * me_stochastic_bf16 -- fp32 -> bf16 with stochastic rounding (micro_engram/optim.py:33-44):
+ * the 16-bit noise is added to the fp32 bit pattern below the kept bits, then the low 16 bits
+ * are dropped; inf and NaN convert as usual. Element i takes the me_sparse_adam noise of
+ * (row i / 4096, column i % 4096, which 0) for stream_id and step. out is bf16 bits [n].
+ */
+int me_stochastic_bf16(const float *x, int64_t n, uint16_t *out, uint64_t seed, uint32_t step,
+                       uint32_t stream_id, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

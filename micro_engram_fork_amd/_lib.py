@@ -30,6 +30,15 @@ SIGNATURES = {
     "me_gate_workspace_size": [c_i64, c_i64, ctypes.POINTER(c_size)],
     "me_gate_residual": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_int,
                          c_ptr, c_ptr, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_size, c_ptr],
+    "me_dedup_workspace_size": [c_i64, ctypes.POINTER(c_size)],
+    "me_dedup": [c_ptr, c_i64, c_i64, c_ptr, c_int, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+                 c_size, c_ptr],
+    "me_sumsq": [c_ptr, c_i64, c_ptr, c_int, c_ptr, c_size, c_ptr],
+    "me_sparse_adam": [c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_int,
+                       c_int, c_int, c_int, c_double, c_double, c_double, c_double, c_double,
+                       c_int, ctypes.c_uint64, c_ptr, c_double, c_ptr],
+    "me_stochastic_bf16": [c_ptr, c_i64, c_ptr, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                           c_ptr],
 }
 
 _lock = threading.Lock()

@@ -225,7 +225,14 @@ class MicroEngram(nn.Module):
 
     def lookup(self, idx):
         """The table rows for the hashed ids: list of n_tables tensors [*idx shape, D]
-        (module.py:146-154)."""
+        (module.py:146-154). Row-sharded tables go through the server's lookup or the
+        differentiable row lookup (sparse row gradients, micro_engram/rows.py:150-161)."""
+        if self.row_shards is not None:
+            if self.row_lookup_fn is not None:
+                return self.row_lookup_fn(self, idx)
+            from .rows import row_lookup
+
+            return row_lookup(self, idx)
         shape = tuple(idx[0].shape)
         mem = self._mem(idx)
         D = self.engram_dim

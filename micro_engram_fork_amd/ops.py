@@ -289,3 +289,108 @@ def library_loaded():
     """Loads the HIP library (raises if it is missing) and returns its path."""
     _lib.load()
     return _lib.lib_path()
+
+
+# ------------------------------------------------------------------------- training side
+def dedup_workspace_bytes(n):
+    size = ctypes.c_size_t(0)
+    call("me_dedup_workspace_size", n, ctypes.byref(size))
+    return size.value
+
+
+@torch.library.custom_op("micro_engram_amd::dedup", mutates_args=())
+def dedup(keys: torch.Tensor, key_bound: int, grads: Optional[torch.Tensor]) -> List[torch.Tensor]:
+    """[uniq [n], inv [n], count [1]] or [uniq, inv, count, gsum [n, D]]: torch.unique(keys,
+    return_inverse=True) with the fp32 index_add_ sums of `grads` (micro_engram/rows.py:81,
+    117-118, 144-146). Only uniq[:count] and gsum[:count] are meaningful."""
+    dev = require_gpu(keys, grads)
+    keys = keys.reshape(-1).long().contiguous()
+    n = keys.numel()
+    uniq = torch.empty(n, dtype=torch.int64, device=dev)
+    inv = torch.empty(n, dtype=torch.int64, device=dev)
+    count = torch.empty(1, dtype=torch.int64, device=dev)
+    gsum, gptr, gcode, dim = None, None, 0, 0
+    if grads is not None:
+        grads = grads.reshape(n, grads.shape[-1] if grads.dim() >= 2 else 1)
+        if grads.dtype not in (torch.float32, torch.bfloat16):
+            grads = grads.float()
+        grads = grads.contiguous()
+        dim = grads.shape[1]
+        gsum = torch.empty((n, dim), dtype=torch.float32, device=dev)
+        gptr, gcode = grads.data_ptr(), dtype_code(grads)
+    ws = torch.empty(max(dedup_workspace_bytes(n), 16), dtype=torch.uint8, device=dev)
+    call("me_dedup", _p(keys), n, key_bound, gptr, gcode, dim, _p(uniq), _p(inv), _p(gsum),
+         count.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(dev))
+    return [uniq, inv, count] if gsum is None else [uniq, inv, count, gsum]
+
+
+@dedup.register_fake
+def _(keys, key_bound, grads):
+    n = keys.numel()
+    outs = [keys.new_empty(n, dtype=torch.int64), keys.new_empty(n, dtype=torch.int64),
+            keys.new_empty(1, dtype=torch.int64)]
+    if grads is not None:
+        outs.append(grads.new_empty((n, grads.shape[-1] if grads.dim() >= 2 else 1), dtype=torch.float32))
+    return outs
+
+
+def sumsq(x, out=None, accumulate=False):
+    """Sum of squares of an fp32 tensor into a device scalar (the squared gradient norm of
+    RowTables.clip, micro_engram/rows.py:214-223)."""
+    dev = require_gpu(x, out)
+    x = x.reshape(-1).float().contiguous()
+    if out is None:
+        out = torch.zeros(1, dtype=torch.float32, device=dev)
+    ws = torch.empty(1024, dtype=torch.uint8, device=dev)
+    call("me_sumsq", _p(x), x.numel(), out.data_ptr(), int(accumulate), ws.data_ptr(), ws.numel(),
+         stream_of(dev))
+    return out
+
+
+def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *, lr, betas, eps,
+                weight_decay, rowwise, lazy, stochastic_rounding, seed, grad_sumsq=None,
+                max_norm=0.0):
+    """One LazyAdamW step on the given rows of each table (micro_engram/optim.py:65-133), all
+    tables in one launch. params/exp_avgs [rows_k, D]; exp_avg_sqs [rows_k] fp32 (row-wise) or
+    like params; rows int64 [n_k] unique; grads fp32 [n_k, D]; steps: step counts after the
+    increment. Updates the tensors in place."""
+    dev = require_gpu(*params, *exp_avgs, *exp_avg_sqs, *rows, *grads, grad_sumsq)
+    n = len(params)
+    if not (len(exp_avgs) == len(exp_avg_sqs) == len(rows) == len(grads) == len(steps) == n):
+        raise ValueError("[micro_engram] sparse_adam: per-table lists differ in length")
+    if n == 0:
+        return
+    dim = params[0].shape[1]
+    pdt = params[0].dtype
+    for p, m, v, r, g in zip(params, exp_avgs, exp_avg_sqs, rows, grads):
+        if p.dim() != 2 or p.shape[1] != dim or p.dtype != pdt or not p.is_contiguous():
+            raise ValueError("[micro_engram] sparse_adam: tables must be contiguous [rows, D] of one dtype")
+        if m.shape != p.shape or m.dtype != pdt or not m.is_contiguous():
+            raise ValueError("[micro_engram] sparse_adam: exp_avg must match its table")
+        want_v = (p.shape[0],) if rowwise else tuple(p.shape)
+        if tuple(v.shape) != want_v or not v.is_contiguous() or (rowwise and v.dtype != torch.float32):
+            raise ValueError("[micro_engram] sparse_adam: exp_avg_sq has the wrong shape or dtype")
+        if r.dtype != torch.int64 or g.dtype != torch.float32 or g.shape != (r.numel(), dim):
+            raise ValueError("[micro_engram] sparse_adam: rows must be int64 [n], grads fp32 [n, D]")
+    rows = [r.contiguous() for r in rows]
+    grads = [g.contiguous() for g in grads]
+    sq_code = dtype_code(exp_avg_sqs[0]) if not rowwise else ME_F32
+    call("me_sparse_adam", n, ptr_array([p.data_ptr() for p in params]),
+         ptr_array([m.data_ptr() for m in exp_avgs]), ptr_array([v.data_ptr() for v in exp_avg_sqs]),
+         ptr_array([r.data_ptr() for r in rows]), ptr_array([g.data_ptr() for g in grads]),
+         i64_array([r.numel() for r in rows]), i64_array([int(s) for s in steps]),
+         i32_array([int(s) for s in stream_ids]), dim, dtype_code(params[0]), int(bool(rowwise)),
+         sq_code, int(bool(lazy)), float(lr), float(betas[0]), float(betas[1]), float(eps),
+         float(weight_decay), int(bool(stochastic_rounding)), int(seed) & ((1 << 64) - 1),
+         _p(grad_sumsq), float(max_norm), stream_of(dev))
+
+
+def stochastic_bf16(x, seed, step=0, stream_id=0):
+    """bf16 tensor like x: fp32 -> bf16 with stochastic rounding (micro_engram/optim.py:33-44);
+    element i uses the noise of (row i // 4096, column i % 4096) of `stream_id` at `step`."""
+    dev = require_gpu(x)
+    xf = x.float().contiguous()
+    out = torch.empty(xf.shape, dtype=torch.bfloat16, device=dev)
+    call("me_stochastic_bf16", xf.data_ptr(), xf.numel(), out.data_ptr(),
+         int(seed) & ((1 << 64) - 1), int(step) & 0xFFFFFFFF, int(stream_id), stream_of(dev))
+    return out

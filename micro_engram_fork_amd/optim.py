@@ -1,0 +1,110 @@
+"""LazyAdamW for the engram tables on MI355X (micro_engram/optim.py:47-133 surface).
+
+AdamW in which, for groups with lazy=True, a table row whose gradient is all zero keeps its
+weights and both moments exactly (like torch.optim.SparseAdam); rowwise=True keeps one fp32
+second moment per row (the running mean of the row's g^2). State names match
+torch.optim.AdamW (step, exp_avg, exp_avg_sq). Row gradients arrive either as
+p.sparse_grad = (unique rows, fp32 [n, D]) (the row-sharded training path,
+micro_engram/rows.py:137-147) or as a dense p.grad.
+
+The update runs as HIP launches of libmicro_engram_amd.so (me_sparse_adam), all tables of a
+parameter group with the same layout in one launch. bf16 weights and moments are written back
+with stochastic rounding whose noise comes from a counter-based generator (Philox4x32-10 keyed
+by `seed`, the table's step and the element's position) instead of torch.randint: the same
+rounding distribution, reproducible for a given seed.
+"""
+import torch
+
+from . import ops
+
+
+def stochastic_bf16(x, seed=None, step=0, stream_id=0):
+    """fp32 -> bf16 with stochastic rounding (micro_engram/optim.py:33-44): the magnitude rounds
+    up with probability equal to the dropped fraction, so on average nothing is lost; inf and
+    NaN are kept. seed None draws one from torch's default generator."""
+    if seed is None:
+        seed = int(torch.randint(0, 2**62, (1,)).item())
+    return ops.stochastic_bf16(x, seed, step, stream_id)
+
+
+class LazyAdamW(torch.optim.Optimizer):
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, lazy=False,
+                 rowwise=False, stochastic_rounding=True, seed=None):
+        """stochastic_rounding: bf16 weights and states are written back with stochastic rounding
+        (fp32 ones are unaffected). seed: key of the rounding noise (drawn from torch's default
+        generator when None)."""
+        super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, lazy=lazy,
+                                      rowwise=rowwise, stochastic_rounding=stochastic_rounding))
+        self.seed = int(torch.randint(0, 2**62, (1,)).item()) if seed is None else int(seed)
+        self._clip = None  # (device squared norm, max_norm) applied by the next step
+
+    @staticmethod
+    def init_state(state, p, group):
+        """Fresh state: exp_avg like p; exp_avg_sq like p, or [rows] fp32 when row-wise
+        (optim.py:55-63)."""
+        state["step"] = torch.zeros((), dtype=torch.float32)
+        state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+        if group.get("rowwise") and p.dim() >= 2:
+            state["exp_avg_sq"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
+        else:
+            state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+
+    def clip_next_step(self, sumsq, max_norm):
+        """Scale the next step's gradients by min(max_norm / (sqrt(sumsq) + 1e-6), 1) inside the
+        update kernel (RowTables.clip, micro_engram/rows.py:224-231); sumsq is a device scalar."""
+        self._clip = (sumsq, float(max_norm))
+
+    @staticmethod
+    def _as_rows(t, n):
+        return t.view(n, -1) if t.dim() >= 2 else t.view(n, 1)
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        index = {id(p): i for i, p in enumerate(p for g in self.param_groups for p in g["params"])}
+        clip, self._clip = self._clip, None
+        for group in self.param_groups:
+            batches = {}
+            for p in group["params"]:
+                sparse = getattr(p, "sparse_grad", None)
+                if p.grad is None and sparse is None:
+                    continue
+                state = self.state[p]
+                if not state:
+                    self.init_state(state, p, group)
+                state["step"] += 1
+                n = p.shape[0] if p.dim() >= 1 else 1
+                rowwise = state["exp_avg_sq"].dim() == 1 and p.dim() >= 2
+                # the reference's lazy branches need rows (p.dim() >= 2); others are plain AdamW
+                lazy = bool(group["lazy"]) and p.dim() >= 2
+                if sparse is not None:
+                    if not group["lazy"]:
+                        raise ValueError("sparse row gradients need lazy=True")
+                    rows, g = sparse[0].long(), sparse[1].float()
+                else:
+                    g = p.grad.float()
+                    rows = torch.arange(n, device=p.device)  # all-zero rows skip in the kernel
+                P = self._as_rows(p.data, n)
+                M = self._as_rows(state["exp_avg"], n)
+                V = state["exp_avg_sq"] if rowwise else self._as_rows(state["exp_avg_sq"], n)
+                key = (P.dtype, P.shape[1], rowwise, lazy, V.dtype)
+                b = batches.setdefault(key, {"params": [], "exp_avgs": [], "exp_avg_sqs": [], "rows": [],
+                                             "grads": [], "steps": [], "stream_ids": []})
+                b["params"].append(P)
+                b["exp_avgs"].append(M)
+                b["exp_avg_sqs"].append(V)
+                b["rows"].append(rows)
+                b["grads"].append(g.reshape(rows.numel(), -1))
+                b["steps"].append(int(state["step"].item()))
+                b["stream_ids"].append(index[id(p)] % 65536)
+            for (_, _, rowwise, lazy, _), b in batches.items():
+                ops.sparse_adam(b["params"], b["exp_avgs"], b["exp_avg_sqs"], b["rows"], b["grads"],
+                                b["steps"], b["stream_ids"], lr=group["lr"], betas=group["betas"],
+                                eps=group["eps"], weight_decay=group["weight_decay"], rowwise=rowwise,
+                                lazy=lazy, stochastic_rounding=group.get("stochastic_rounding", True),
+                                seed=self.seed, grad_sumsq=clip[0] if clip else None,
+                                max_norm=clip[1] if clip else 0.0)
+        return loss

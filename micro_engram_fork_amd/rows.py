@@ -1,0 +1,168 @@
+"""Row tables on one GPU: touched-row dedup, coalesced sparse gradients, clipping and the row
+optimizer (the surface of micro_engram/rows.py at world size 1).
+
+With one GPU every table is whole in HBM, so the reference's all_to_all row exchange
+(rows.py:57-134) reduces to: gather the rows, and in the backward sum the gradient rows of
+equal (table, row) keys -- torch.unique + index_add_ in the reference (rows.py:81, 117-118),
+the radix-sort dedup kernel here (bit-exact: same unique keys, inverse and fp32 sums) -- and
+keep them per table as p.sparse_grad = (unique rows, fp32 sums) (rows.py:137-147). More than one
+rank needs that exchange, which this single-GPU build does not provide; it raises.
+"""
+import torch
+
+from . import ops
+from .optim import LazyAdamW
+
+
+def row_range(n_rows, rank, world):
+    """(first row, row count) owned by `rank`: ceil(n / world) rows each (rows.py:39-44)."""
+    per = -(-n_rows // world)
+    start = min(rank * per, n_rows)
+    return start, max(0, min(per, n_rows - start))
+
+
+def dedup_rows(keys, key_bound, grads=None):
+    """(unique keys ascending, inverse, fp32 sums of `grads` per unique key) -- torch.unique(
+    return_inverse=True) + zeros().index_add_(0, inv, grads.float()) (rows.py:81, 117-118),
+    bit-exact. Reads the unique count back to the host (the reference syncs here too,
+    rows.py:92)."""
+    outs = ops.dedup(keys, int(key_bound), grads)
+    n = int(outs[2].item())
+    uniq, inv = outs[0][:n], outs[1]
+    return (uniq, inv, outs[3][:n]) if grads is not None else (uniq, inv, None)
+
+
+def add_sparse_grad(p, rows, g):
+    """Add gradient rows `g` [n, dim] for local rows `rows` to p.sparse_grad, kept coalesced:
+    (unique rows, their fp32 sums), the previous entries first (rows.py:137-147)."""
+    cur = getattr(p, "sparse_grad", None)
+    if cur is not None:
+        rows, g = torch.cat([cur[0], rows]), torch.cat([cur[1], g])
+    u, _, acc = dedup_rows(rows.long(), p.shape[0], g.float())
+    p.sparse_grad = (u, acc)
+
+
+def _table_offsets(engram):
+    offs = [0]
+    for rows in engram.table_rows:
+        offs.append(offs[-1] + rows)
+    return offs
+
+
+class _RowLookup(torch.autograd.Function):
+    """Per-table rows for hashed ids, world size 1. Backward: the gradient rows of every lookup
+    are deduplicated over (table, row) and added to each shard's sparse gradient (shards marked
+    _sparse_rows) or to a dense gradient (rows.py:71-134)."""
+
+    @staticmethod
+    def forward(ctx, idx2d, offsets, *shards):
+        mem = ops.gather(idx2d, [s.detach() for s in shards])
+        ctx.save_for_backward(idx2d)
+        ctx.offsets = offsets
+        ctx.shapes = [(s.shape, s.dtype) for s in shards]
+        ctx.shards = shards if any(getattr(s, "_sparse_rows", False) for s in shards) else None
+        return mem
+
+    @staticmethod
+    def backward(ctx, grad):
+        (idx2d,) = ctx.saved_tensors
+        nt, n = idx2d.shape
+        D = ctx.shapes[0][0][1]
+        offs = torch.tensor(ctx.offsets[:-1], dtype=torch.int64, device=idx2d.device)
+        # token-major flattening: lookup i*nt + k is (token i, table k), whose gradient row is
+        # grad[i, k*D:(k+1)*D]; equal keys share a table, so within a key this is token order,
+        # the order of the reference's table-major flattening
+        keys = (idx2d + offs[:, None]).t().reshape(-1)
+        uniq, _, gsum = dedup_rows(keys, ctx.offsets[-1], grad.reshape(n * nt, D))
+        bounds = torch.searchsorted(uniq, torch.tensor(ctx.offsets, device=uniq.device)).tolist()
+        grads = []
+        for k, (shape, dtype) in enumerate(ctx.shapes):
+            if not ctx.needs_input_grad[2 + k]:
+                grads.append(None)
+                continue
+            a, b = bounds[k], bounds[k + 1]
+            local = uniq[a:b] - ctx.offsets[k]
+            if ctx.shards is not None and getattr(ctx.shards[k], "_sparse_rows", False):
+                add_sparse_grad(ctx.shards[k], local, gsum[a:b])
+                grads.append(None)
+                continue
+            g = torch.zeros(shape, dtype=torch.float32, device=grad.device)
+            g[local] = gsum[a:b]  # unique rows: a plain scatter
+            grads.append(g.to(dtype))
+        return (None, None, *grads)
+
+
+def row_lookup(engram, idx):
+    """Per-table rows [*idx shape, dim] for the hashed ids `idx` (rows.py:150-161), world 1."""
+    shards = engram.row_shards
+    _rank, world, _starts, _pers = engram.row_info
+    if world != 1:
+        raise NotImplementedError("[micro_engram] row-sharded lookup over several ranks needs the "
+                                  "multi-GPU row exchange, not part of this single-GPU build")
+    idx2d = engram._stacked_idx(idx)
+    mem = _RowLookup.apply(idx2d, _table_offsets(engram), *shards)
+    D = engram.engram_dim
+    shape = tuple(idx[0].shape)
+    return [mem[:, k * D:(k + 1) * D].reshape(*shape, D) for k in range(len(shards))]
+
+
+class RowTables:
+    """The engrams' row tables on one GPU: optimizer, clipping (rows.py:179-247). entries:
+    [(prefix, engram)] with row shards (MicroEngram.shard_rows(0, 1))."""
+
+    def __init__(self, entries, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, lazy=False,
+                 rowwise=False, stochastic_rounding=True, sparse_grads=False, seed=None):
+        self.entries = entries
+        self.world = 1
+        train = [p for _, e in entries for p in e.row_shards if p.requires_grad]
+        if sparse_grads and not lazy:
+            raise ValueError("sparse row gradients need a lazy optimizer (lazy_adam / rowwise_adam): "
+                             "plain AdamW updates every row every step")
+        self.sparse = bool(sparse_grads)
+        for p in train:
+            p._sparse_rows = self.sparse
+        self.optimizer = LazyAdamW([{"params": train, "lazy": lazy, "rowwise": rowwise}], lr=lr, betas=betas,
+                                   eps=eps, weight_decay=weight_decay, stochastic_rounding=stochastic_rounding,
+                                   seed=seed) if train else None
+        self.last_grad_norm = None
+
+    def params(self):
+        return [p for _, e in self.entries for p in e.row_shards]
+
+    def clip(self, max_norm):
+        """Global norm of the table gradients; the next step scales them to max_norm if larger
+        (rows.py:208-233). Returns the norm (a host read, as in the reference)."""
+        ps = [p for p in self.params() if p.requires_grad]
+        if not ps:
+            return None
+        sq = torch.zeros(1, dtype=torch.float32, device=ps[0].device)
+        for p in ps:
+            if p.grad is not None:
+                ops.sumsq(p.grad, sq, accumulate=True)
+            sg = getattr(p, "sparse_grad", None)
+            if sg is not None:
+                ops.sumsq(sg[1], sq, accumulate=True)
+        if max_norm and max_norm > 0 and self.optimizer is not None:
+            self.optimizer.clip_next_step(sq, max_norm)
+        self.last_grad_norm = float(sq.sqrt().item())
+        return self.last_grad_norm
+
+    def step(self, lr):
+        if self.optimizer is None:
+            return
+        for g in self.optimizer.param_groups:
+            g["lr"] = lr
+        self.optimizer.step()
+        self.zero_grad()
+
+    def zero_grad(self):
+        if self.optimizer is not None:
+            self.optimizer.zero_grad(set_to_none=True)
+        for p in self.params():
+            p.sparse_grad = None
+
+    def save(self, folder, optim_folder=None):
+        raise NotImplementedError("[micro_engram] DCP checkpoints of the row tables are not part of this build")
+
+    def load(self, folder, optim_folder=None):
+        raise NotImplementedError("[micro_engram] DCP checkpoints of the row tables are not part of this build")

@@ -230,9 +230,9 @@ def philox4x32_10(ctr, key):
 def sr_noise(seed, step, table, rows, dim, which):
     """The 16-bit rounding noise of the HIP rowwise-Adam kernel, int32 [len(rows), dim].
 
-    Element (row, col) of array `which` (0: weights, 1: first moment) of table `table` at
-    optimizer step `step` takes 16 bits of Philox4x32-10 with
-      counter = (row & 0xffffffff, row >> 32, step, table << 16 | which << 15 | col >> 3)
+    Element (row, col) of array `which` (0: weights, 1: first moment, 2: per-value second
+    moment) of table `table` at optimizer step `step` takes 16 bits of Philox4x32-10 with
+      counter = (row & 0xffffffff, row >> 32, step, table << 16 | which << 14 | col >> 3)
       key     = (seed & 0xffffffff, seed >> 32)
     word (col >> 1) & 3, half col & 1."""
     rows = np.asarray(rows, dtype=np.int64).astype(np.uint64)
@@ -242,7 +242,7 @@ def sr_noise(seed, step, table, rows, dim, which):
     ctr[..., 0] = (rows & np.uint64(0xFFFFFFFF)).astype(np.uint32)[:, None]
     ctr[..., 1] = (rows >> np.uint64(32)).astype(np.uint32)[:, None]
     ctr[..., 2] = np.uint32(step & 0xFFFFFFFF)
-    ctr[..., 3] = ((np.uint64(table) << np.uint64(16)) | (np.uint64(which) << np.uint64(15))
+    ctr[..., 3] = ((np.uint64(table) << np.uint64(16)) | (np.uint64(which) << np.uint64(14))
                    | (cols >> np.uint64(3))).astype(np.uint32)[None, :]
     key = np.empty((R, dim, 2), dtype=np.uint32)
     key[..., 0] = np.uint32(seed & 0xFFFFFFFF)
@@ -271,7 +271,7 @@ def sparse_adam_step(p, m, v, rows, g, step, lr, betas=(0.9, 0.999), eps=1e-8, w
     109-132). p [R, D] and m like p (bf16 or fp32), v [R] fp32 (row-wise) or like p; rows int64
     unique ascending with fp32 g [U, D]; step = the step count after this step's increment.
     noise(rows, which) -> int32 [len(rows), D] supplies the bf16 rounding noise (which 0: p,
-    1: m). Returns the rows that were updated."""
+    1: m, 2: a per-value v). Returns the rows that were updated."""
     beta1, beta2 = betas
     bc1, bc2 = 1 - beta1 ** step, 1 - beta2 ** step
     keep = (g != 0).flatten(1).any(dim=1)
@@ -298,7 +298,7 @@ def sparse_adam_step(p, m, v, rows, g, step, lr, betas=(0.9, 0.999), eps=1e-8, w
 
     p.index_copy_(0, rows, cast(p_, p.dtype, 0))
     m.index_copy_(0, rows, cast(m_, m.dtype, 1))
-    v.index_copy_(0, rows, v_.to(v.dtype))
+    v.index_copy_(0, rows, cast(v_, v.dtype, 2))
     return rows
 
 

@@ -1,0 +1,304 @@
+"""Stage 4 on the GPU against the oracle: dedup bit-exact (unique keys, inverse, fp32 sums),
+the squared norm, stochastic rounding and the sparse LazyAdamW step.
+
+Tolerance of the Adam step: the GPU and the oracle draw identical rounding noise, so bf16
+results are equal except where the fp32 value before rounding differs in its last bits (the
+row mean of g^2 is summed in another order) and the noise sits right at the boundary: at most
+1e-4 of the elements may differ, each by exactly one bf16 step; fp32 values within 2e-6
+relative plus a few fp32 ulps of the pre-update magnitude; the row-wise second moment within
+1e-6 relative. A bf16 element that an update cancels to near zero may differ by more steps,
+within 2e-8 absolute (a few fp32 ulps of the ~0.02 operands).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from micro_engram_fork_amd import MicroEngram, ops, rows as me_rows, synthetic
+from micro_engram_fork_amd.optim import LazyAdamW, stochastic_bf16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check_dedup(keys, grads, key_bound):
+    uniq, inv, gsum = me_rows.dedup_rows(keys.to(DEV), key_bound, None if grads is None else grads.to(DEV))
+    g_np = grads.float().numpy() if grads is not None else np.zeros((keys.numel(), 1), np.float32)
+    u, i, acc = oracle.dedup(keys.numpy(), g_np)
+    assert np.array_equal(uniq.cpu().numpy(), u)
+    assert np.array_equal(inv.cpu().numpy(), i)
+    if grads is not None:
+        assert np.array_equal(gsum.cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
+@pytest.mark.parametrize("n,bound,dim", [(1, 5, 4), (37, 3, 4), (2048, 100, 8), (2049, 100, 3),
+                                         (10000, 1 << 20, 64), (5000, 1 << 40, 16)])
+def test_dedup_bit_exact(n, bound, dim):
+    g = torch.Generator().manual_seed(n)
+    keys = torch.randint(0, bound, (n,), generator=g)
+    if n > 100:
+        keys[::3] = keys[0]  # one key repeated across blocks and passes
+    grads = torch.randn(n, dim, generator=g) * torch.logspace(-4, 2, n).unsqueeze(1)
+    _check_dedup(keys, grads, bound)
+
+
+def test_dedup_bf16_grads_and_keys_only():
+    g = torch.Generator().manual_seed(1)
+    keys = torch.randint(0, 300, (4000,), generator=g)
+    _check_dedup(keys, (torch.randn(4000, 32, generator=g)).bfloat16(), 300)
+    _check_dedup(keys, None, 300)
+
+
+def test_dedup_empty():
+    uniq, inv, gsum = me_rows.dedup_rows(torch.zeros(0, dtype=torch.long, device=DEV), 10,
+                                         torch.zeros(0, 4, device=DEV))
+    assert uniq.numel() == 0 and inv.numel() == 0 and gsum.shape == (0, 4)
+
+
+def test_add_sparse_grad_merges_like_reference():
+    # rows.py:137-147: earlier entries first, then unique + index_add_
+    p = torch.zeros(50, 8, device=DEV)
+    g = torch.Generator().manual_seed(2)
+    r1, g1 = torch.randint(0, 50, (30,), generator=g), torch.randn(30, 8, generator=g)
+    r2, g2 = torch.randint(0, 50, (40,), generator=g), torch.randn(40, 8, generator=g)
+    me_rows.add_sparse_grad(p, r1.to(DEV), g1.to(DEV))
+    me_rows.add_sparse_grad(p, r2.to(DEV), g2.to(DEV))
+    u1, _, a1 = oracle.dedup(r1.numpy(), g1.numpy())
+    u, _, a = oracle.dedup(np.concatenate([u1, r2.numpy()]), np.concatenate([a1, g2.numpy()]))
+    assert np.array_equal(p.sparse_grad[0].cpu().numpy(), u)
+    assert np.array_equal(p.sparse_grad[1].cpu().numpy().view(np.int32), a.view(np.int32))
+
+
+def test_sumsq():
+    x = torch.randn(123457, device=DEV)
+    got = float(ops.sumsq(x))
+    want = float((x.double() ** 2).sum())
+    assert abs(got - want) <= 1e-5 * want
+
+
+def test_stochastic_bf16_matches_oracle_noise():
+    x = torch.randn(10000) * 3
+    seed, step, stream = 99, 4, 7
+    got = stochastic_bf16(x.to(DEV), seed=seed, step=step, stream_id=stream).cpu()
+    rows = np.arange(3)  # element i -> (row i // 4096, col i % 4096)
+    noise = oracle.sr_noise(seed, step, stream, rows, 4096, 0).reshape(-1)[:10000]
+    want = oracle.stochastic_bf16(x, torch.from_numpy(noise))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    special = torch.tensor([float("inf"), -float("inf"), 0.0, -0.0], device=DEV)
+    assert torch.equal(stochastic_bf16(special, seed=1).float().cpu(), special.cpu())
+
+
+def test_stochastic_bf16_unbiased():
+    # test_optim.py:115-120
+    for x in (1.00149, -1.00149):
+        out = stochastic_bf16(torch.full((100_000,), x, device=DEV), seed=5).float()
+        assert abs(float(out.mean()) - x) < 2e-5
+
+
+def _adam_case(dtype, rowwise, R=300, D=64, n=120, steps=3, wd=0.0, sr=True, seed=123, lazy=True):
+    g = torch.Generator().manual_seed(R + D)
+    init = (torch.randn(R, D, generator=g) * 0.02).to(dtype)
+    p_gpu = init.clone().to(DEV)
+    m_gpu = torch.zeros_like(p_gpu)
+    v_gpu = torch.zeros(R, device=DEV) if rowwise else torch.zeros_like(p_gpu)
+    p_ref, m_ref = init.clone(), torch.zeros_like(init)
+    v_ref = torch.zeros(R) if rowwise else torch.zeros_like(init)
+    for step in range(1, steps + 1):
+        rows = torch.randperm(R, generator=g)[:n].sort().values
+        grads = torch.randn(n, D, generator=g) * 1e-3
+        grads[::7] = 0  # untouched rows inside the list
+        ops.sparse_adam([p_gpu], [m_gpu], [v_gpu], [rows.to(DEV)], [grads.to(DEV)], [step], [3],
+                        lr=5e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd, rowwise=rowwise,
+                        lazy=lazy, stochastic_rounding=sr, seed=seed)
+
+        def noise(r, which, step=step):
+            return torch.from_numpy(oracle.sr_noise(seed, step, 3, r.numpy(), D, which))
+
+        oracle.sparse_adam_step(p_ref, m_ref, v_ref, rows, grads, step, 5e-3, (0.9, 0.999), 1e-8, wd,
+                                stochastic_rounding=sr, noise=noise)
+    return (p_gpu.cpu(), m_gpu.cpu(), v_gpu.cpu()), (p_ref, m_ref, v_ref)
+
+
+def _assert_bf16_close(got, want, frac=1e-4, atol=2e-8):
+    # a result that an update cancels to ~1e-8 inherits the fp32 rounding of the ~0.02 operands
+    # (ulp 2e-9), many bf16 steps at that magnitude: such elements pass on the absolute bound
+    diff = got.view(torch.int16).int() - want.view(torch.int16).int()
+    far = (diff.abs() > 1) & ((got.float() - want.float()).abs() > atol)
+    assert not far.any(), f"{int(far.sum())} bf16 results differ by more than one step and {atol}"
+    assert (diff != 0).float().mean() <= frac
+
+
+@pytest.mark.parametrize("rowwise", [True, False])
+@pytest.mark.parametrize("wd", [0.0, 0.01])
+def test_sparse_adam_bf16_matches_oracle(rowwise, wd):
+    (p, m, v), (pr, mr, vr) = _adam_case(torch.bfloat16, rowwise, wd=wd)
+    _assert_bf16_close(p, pr)
+    _assert_bf16_close(m, mr)
+    if rowwise:
+        assert torch.allclose(v, vr, rtol=1e-6, atol=0)
+    else:
+        _assert_bf16_close(v, vr)
+
+
+def _assert_fp32_close(got, want, rtol, atol):
+    err = (got - want).abs() - rtol * want.abs()
+    assert float(err.max()) <= atol, f"max excess {float(err.max()):.3e} over rtol {rtol} + atol {atol}"
+
+
+def test_sparse_adam_fp32_matches_oracle():
+    # weights ~0.02 carry an fp32 rounding of ulp(0.05) ~ 4e-9 per step; one that an update
+    # cancels toward zero keeps that as absolute error, hence atol = 3 steps x 4 ulps of 0.05
+    (p, m, v), (pr, mr, vr) = _adam_case(torch.float32, True, sr=True)
+    _assert_fp32_close(p, pr, 2e-6, 5e-8)
+    _assert_fp32_close(m, mr, 2e-6, 1e-10)  # m ~1e-4: a few ulps of 1e-4
+    _assert_fp32_close(v, vr, 1e-6, 0.0)
+
+
+def test_lazy_adamw_api_and_invariants():
+    # test_optim.py:56-88 through the optimizer class: state names, untouched rows exact
+    torch.manual_seed(0)
+    R, C = 16, 8
+    init = torch.randn(R, C)
+    p = torch.nn.Parameter(init.clone().to(DEV))
+    opt = LazyAdamW([p], lr=1e-2, lazy=True, rowwise=True, seed=1)
+    for i in range(5):
+        gr = torch.randn(R, C)
+        gr[4:] = 0
+        if i > 0:
+            gr[0] = 0
+        p.grad = gr.to(DEV)
+        opt.step()
+    st = opt.state[p]
+    assert set(st) == {"step", "exp_avg", "exp_avg_sq"} and float(st["step"]) == 5
+    assert st["exp_avg_sq"].shape == (R,) and st["exp_avg_sq"].dtype == torch.float32
+    assert torch.equal(p.detach()[4:].cpu(), init[4:])
+    assert torch.equal(st["exp_avg"][4:].cpu(), torch.zeros(R - 4, C))
+
+
+def test_rowwise_equals_adamw_uniform_rows():
+    # test_optim.py:74-80 through LazyAdamW (non-lazy rowwise, fp32)
+    torch.manual_seed(1)
+    R, C = 16, 8
+    init = torch.randn(R, C)
+    row_scale = torch.rand(R, 1) + 0.5
+    grads = [row_scale * torch.sign(torch.randn(R, C)) * (i + 1) for i in range(5)]
+    a = torch.nn.Parameter(init.clone())
+    ta = torch.optim.AdamW([a], lr=1e-2, weight_decay=0.1, foreach=False)
+    b = torch.nn.Parameter(init.clone().to(DEV))
+    tb = LazyAdamW([b], lr=1e-2, weight_decay=0.1, lazy=False, rowwise=True)
+    for gr in grads:
+        a.grad, b.grad = gr.clone(), gr.clone().to(DEV)
+        ta.step()
+        tb.step()
+    assert torch.allclose(a.detach(), b.detach().cpu(), atol=1e-6)
+
+
+def test_bf16_stochastic_rounding_tracks_fp32():
+    # test_optim.py:121-136: at a low learning rate bf16 + SR moves like fp32, plain rounding not
+    moved = {}
+    for name, dtype, sr in (("fp32", torch.float32, True), ("plain", torch.bfloat16, False),
+                            ("sr", torch.bfloat16, True)):
+        w = torch.nn.Parameter(torch.full((2000, 8), 0.03, dtype=dtype, device=DEV))
+        opt = LazyAdamW([{"params": [w], "lazy": True, "rowwise": True}], lr=2.5e-5, stochastic_rounding=sr,
+                        seed=7)
+        for _ in range(300):
+            w.grad = torch.ones_like(w)
+            opt.step()
+        moved[name] = float((0.03 - w.float()).mean())
+    assert abs(moved["plain"] / moved["fp32"] - 1) > 0.2
+    assert abs(moved["sr"] / moved["fp32"] - 1) < 0.03
+
+
+def test_row_lookup_backward_sparse_grads():
+    eng = MicroEngram(model_dim=16, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3),
+                      vocab_size=500, seed=3)
+    shards = eng.shard_rows(0, 1, device=DEV)
+    for s in shards:
+        s._sparse_rows = True
+    ids = torch.randint(0, 500, (2, 40), device=DEV)
+    idx = eng.hash_ids(ids)
+    out = me_rows.row_lookup(eng, idx)
+    grads = [torch.randn_like(o) for o in out]
+    torch.autograd.backward(out, grads)
+    for k, s in enumerate(shards):
+        u, _, acc = oracle.dedup(idx[k].reshape(-1).cpu().numpy(), grads[k].reshape(-1, 8).cpu().numpy())
+        assert np.array_equal(s.sparse_grad[0].cpu().numpy(), u)
+        assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
+def test_row_tables_clip_scales_next_step():
+    eng = MicroEngram(model_dim=16, table_size=64, engram_dim=8, num_heads=1, orders=(2,), vocab_size=50)
+    shards = eng.shard_rows(0, 1, device=DEV)
+    rt = me_rows.RowTables([("x.", eng)], lr=1e-1, lazy=True, rowwise=True, sparse_grads=True,
+                           stochastic_rounding=False, seed=0)
+    before = shards[0].detach().clone()
+    rows = torch.tensor([1, 5, 9], device=DEV)
+    g = torch.full((3, 8), 3.0, device=DEV)
+    me_rows.add_sparse_grad(shards[0], rows, g)
+    norm = rt.clip(1.0)
+    assert abs(norm - (9 * 24) ** 0.5) < 1e-4
+    rt.step(1e-1)
+    assert shards[0].sparse_grad is None
+    moved = (shards[0].detach() - before).abs().sum(1)
+    assert (moved[[1, 5, 9]] > 0).all() and moved.sum() == moved[[1, 5, 9]].sum()
+
+
+# ------------------------------------------------------------ the sparse-update workload
+def test_sparse_update_workload():
+    """The Gemma prefill batch's 196,608 (table, row) lookups with fp32 gradients N(0, 1e-3):
+    dedup bit-exact, then one row-wise Adam step (lr 5e-3, betas 0.9/0.999, eps 1e-8) on the
+    bf16 tables with stochastic rounding, against the oracle drawing the same noise."""
+    eng = synthetic.build_engram("gemma", DEV, seed=0)
+    ids, pos, _ = synthetic.prefill_inputs(seed=0, device=DEV)
+    idx = torch.stack(eng.hash_ids(ids, pos)).reshape(len(eng.tables), -1)
+    offs = [0]
+    for r in eng.table_rows:
+        offs.append(offs[-1] + r)
+    keys = (idx + torch.tensor(offs[:-1], device=DEV)[:, None]).t().reshape(-1)
+    grads = synthetic.lookup_grads(keys.numel(), eng.engram_dim, seed=0, device=DEV)
+    uniq, inv, gsum = me_rows.dedup_rows(keys, offs[-1], grads)
+    u, i, acc = oracle.dedup(keys.cpu().numpy(), grads.cpu().numpy())
+    assert np.array_equal(uniq.cpu().numpy(), u) and np.array_equal(inv.cpu().numpy(), i)
+    assert np.array_equal(gsum.cpu().numpy().view(np.int32), acc.view(np.int32))
+
+    bounds = np.searchsorted(u, np.array(offs))
+    tables = [t.weight for t in eng.tables]
+    before = [t.detach()[torch.from_numpy(u[bounds[k]:bounds[k + 1]] - offs[k]).to(DEV)].cpu()
+              for k, t in enumerate(tables)]
+    opt = LazyAdamW([{"params": tables, "lazy": True, "rowwise": True}], lr=5e-3, seed=2024)
+    for k, t in enumerate(tables):
+        t.sparse_grad = (uniq[bounds[k]:bounds[k + 1]] - offs[k], gsum[bounds[k]:bounds[k + 1]])
+    opt.step()
+    for k, t in enumerate(tables):
+        rows = torch.from_numpy(u[bounds[k]:bounds[k + 1]] - offs[k])
+        p_ref = before[k].clone()
+        m_ref = torch.zeros_like(p_ref)
+        v_ref = torch.zeros(rows.numel())
+
+        def noise(r, which, rows=rows, k=k):
+            return torch.from_numpy(oracle.sr_noise(2024, 1, k, rows[r].numpy(), 64, which))
+
+        oracle.sparse_adam_step(p_ref, m_ref, v_ref, torch.arange(rows.numel()),
+                                torch.from_numpy(acc[bounds[k]:bounds[k + 1]]), 1, 5e-3,
+                                stochastic_rounding=True, noise=noise)
+        got = t.detach()[rows.to(DEV)].cpu()
+        _assert_bf16_close(got, p_ref)
+        _assert_bf16_close(opt.state[t]["exp_avg"][rows.to(DEV)].cpu(), m_ref)
+        assert torch.allclose(opt.state[t]["exp_avg_sq"][rows.to(DEV)].cpu(), v_ref, rtol=1e-6, atol=0)
+    del eng, opt
+    torch.cuda.empty_cache()
+
+
+def test_bf16_second_moment_freeze_vs_stochastic_rounding():
+    # test_optim.py:92-110 through LazyAdamW on the GPU
+    torch.manual_seed(0)
+    init = torch.randn(16, 8).bfloat16()
+    out = {}
+    for name, kw in (("plain", dict(stochastic_rounding=False)), ("sr", {}), ("rowwise", dict(rowwise=True))):
+        p = torch.nn.Parameter(init.clone().to(DEV))
+        opt = LazyAdamW([p], lr=0.0, seed=3, **kw)
+        for _ in range(1500):
+            p.grad = torch.ones_like(p)
+            opt.step()
+        out[name] = float(opt.state[p]["exp_avg_sq"].float().mean()) / (1 - 0.999 ** 1500)
+    assert out["plain"] < 0.5 and abs(out["sr"] - 1) < 0.02 and abs(out["rowwise"] - 1) < 1e-4
