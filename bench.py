@@ -10,10 +10,13 @@ all inputs already in HBM. Prints one JSON line:
 
   value         forward tokens/s over the K timed steps (wall clock, synchronised)
   roofline      the gather kernel (the metric's HBM figure): algorithmic bytes per launch /
-                its mean duration (launches captured in a HIP graph, replayed between two HIP
-                events on the replay stream), against 8 TB/s
-  roofline_gate the K/V projection kernels: 4 * M * d FLOP per token / their mean duration,
-                against 2.5 PFLOP/s dense bf16
+                its mean duration, against 8 TB/s. Timed as a HIP graph of launches over 16
+                distinct prefill batches of the same shape, replayed between HIP events on the
+                replay stream, so that each launch meets caches holding other rows as it does
+                in a step. copy_1gib_gbs: a 1 GiB device copy, the achievable-bandwidth
+                reference and the known-size kernel that calibrates the HBM byte counters
+  roofline_gate the K/V projection kernels: 4 * M * d FLOP per token / their mean duration
+                (graph replay), against 2.5 PFLOP/s dense bf16
   cpu_baseline  the oracle's torch-CPU forward on a token sample of the same batch
 """
 import argparse
@@ -40,11 +43,20 @@ def parse():
     return ap.parse_args()
 
 
-def gather_bytes_per_token(eng, esize):
+# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,100.2
+# KiB per dispatch, x2.0) and WRITE_SIZE (24,580.9 KiB, x1.0), the factors being what the two
+# counters read for this script's 1 GiB device copy. A counter run cannot share a process with
+# the timing, so the figure is a measured constant, re-measured when the kernel changes.
+GATHER_TRAFFIC_BYTES = 49_951_520
+GATHER_CYCLE = 16  # distinct prefill batches the gather timing cycles through
+
+
+def gather_bytes_per_token(eng, esize, canon_read):
     """Algorithmic bytes of the fused hash + gather per token: every table row read and written
-    once, plus the token id, its position and one canon entry (8 bytes each)."""
+    once, plus the token id and its position, and one canon entry when the map is not the
+    identity (8 bytes each)."""
     n_t = len(eng.table_rows)
-    return n_t * eng.engram_dim * esize * 2 + 24
+    return n_t * eng.engram_dim * esize * 2 + 16 + (8 if canon_read else 0)
 
 
 def cpu_baseline(eng, ids, pos, hidden, target_s):
@@ -108,19 +120,21 @@ def main():
         mem = eng.hashed_memory(ids, pos, dev)
         return eng.gate_residual(hidden, mem)
 
-    def kernel_ms(fn, reps):
-        """Mean duration of `fn`'s kernels: `reps` calls captured in one HIP graph, replayed
-        between two HIP events on the replay stream (graph replay keeps host dispatch out of
-        the measurement)."""
+    def replay_ms(fns, reps):
+        """Mean duration of one round of the calls `fns`: `reps` rounds captured in one HIP
+        graph, replayed between two HIP events on the replay stream (consecutive kernels of a
+        graph start back to back, so the events add nothing per round)."""
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            fn()
+            for fn in fns:
+                fn()
             torch.cuda.synchronize()
             with torch.cuda.graph(graph, stream=side):
                 for _ in range(reps):
-                    fn()
+                    for fn in fns:
+                        fn()
             graph.replay()
             torch.cuda.synchronize()
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -140,14 +154,29 @@ def main():
             step()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        # per-kernel timing of the two stages on the same inputs
+
+        # Kernel durations. In a step the gather meets caches that hold other data (the gate
+        # has just streamed ~200 MB through them); replayed on one batch, every launch would
+        # find the previous launch's rows still cached. So the gather is replayed over a cycle
+        # of 16 prefill batches of this shape (seeds 0-15, ~400 MB of rows, more than the
+        # 256 MB last-level cache): each launch reads rows the previous ones have not left
+        # behind, as consecutive prefill batches do.
+        cycle = [synthetic.prefill_ids(seed=s, device=dev) for s in range(GATHER_CYCLE)]
+        gathers = [(lambda i=i, p=p: eng.hashed_memory(i, p, dev)) for i, p in cycle]
+        gather_ms = replay_ms(gathers, 2) / len(gathers)
+        del cycle, gathers
         mem = eng.hashed_memory(ids, pos, dev)
-        gather_ms = kernel_ms(lambda: eng.hashed_memory(ids, pos, dev), 20)
-        gate_ms = kernel_ms(lambda: eng.gate_residual(hidden, mem), 10)
+        gate_ms = replay_ms([lambda: eng.gate_residual(hidden, mem)], 10)
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        copy_ms = replay_ms([lambda: dst.copy_(src)], 5)
+        del src, dst
 
     esize = eng.tables[0].weight.element_size()
-    gbytes = gather_bytes_per_token(eng, esize) * T
+    canon_read = not eng.identity_canon()
+    gbytes = gather_bytes_per_token(eng, esize, canon_read) * T
     gather_gbs = gbytes / (gather_ms * 1e-3) / 1e9
+    copy_gbs = 2.0 * (1 << 30) / (copy_ms * 1e-3) / 1e9
     M = len(eng.table_rows) * eng.engram_dim
     d = hidden.shape[-1]
     gate_flop = 4.0 * M * d * T
@@ -180,12 +209,14 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": gather_gbs / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": GATHER_TRAFFIC_BYTES,
             "bytes_per_launch": gbytes,
+            "canon_read": canon_read,
             "mean_ms": gather_ms,
+            "copy_1gib_gbs": copy_gbs,
         },
         "roofline_gate": {
-            "kernel": "K/V projection + gate + residual (gate_kernel key + value passes)",
+            "kernel": "K/V projection + gate + residual (gate_kernel key + value passes, alpha)",
             "bound": "mfma",
             "achieved": gate_tflops,
             "peak": BF16_PEAK_TFLOPS,

@@ -65,7 +65,9 @@ int me_version(void);
  *   position_ids   nullable; pos_dtype ME_I32/ME_I64; element (b, t) at
  *                  position_ids[b * pos_batch_stride + t] (stride 0 broadcasts one row,
  *                  like position_ids.expand_as(ids) in the reference)
- *   canon          int64 [vocab]; ids are clamped to [0, vocab) before the lookup
+ *   canon          int64 [vocab], or NULL for the identity map (canon[i] == i, the buffer the
+ *                  reference builds when no canon map is given, module.py:101-107); ids are
+ *                  clamped to [0, vocab) before the lookup
  *   mults          int64 [n_tables, max_order]
  *   table_orders   HOST int32 [n_tables]; table_rows HOST int64 [n_tables]
  *   idx_out        int64 [n_tables, batch * seq_len]: idx_out[k][b*seq_len+t] is the row of

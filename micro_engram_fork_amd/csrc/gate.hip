@@ -40,6 +40,8 @@
 namespace me {
 namespace {
 
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef int int32x4 __attribute__((ext_vector_type(4)));
@@ -433,10 +435,13 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 #pragma unroll
                     for (int e = 0; e < kLaneCols; ++e)
                         ov[e] = from_f<H>(to_f<H>(xv[e]) + round_t<H>(alpha * to_f<T>(cv[e])));
+                    // non-temporal: the output is not read again by this kernel, and written
+                    // through it leaves no dirty lines for the next kernel's traffic to evict
                     uint8_t *p = a.out + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
 #pragma unroll
                     for (int q = 0; q < kRowWords; q += 2)
-                        reinterpret_cast<uint2 *>(p)[q / 2] = make_uint2(ow[q], ow[q + 1]);
+                        __builtin_nontemporal_store(u32x2_t{ow[q], ow[q + 1]},
+                                                    reinterpret_cast<u32x2_t *>(p) + q / 2);
                 }
             }
         }

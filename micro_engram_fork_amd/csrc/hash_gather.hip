@@ -10,6 +10,8 @@
 //
 // Kernel layout. One 256-thread workgroup owns `tpb` consecutive tokens (tpb * n_tables <= 256,
 // so every (token, table) pair has a thread):
+//   phase 0  each (token, table) thread loads its table's constants (multipliers, order, fastmod
+//            magic, base address) into registers, before and independent of the token loads;
 //   phase 1  each (token, slot) thread loads one n-gram token, applies clamp + canon and the
 //            pad rules, and leaves the value in LDS (tok[token][slot]);
 //   phase 2  each (token, table) thread hashes its n-gram, writes the int64 row id (coalesced
@@ -17,8 +19,15 @@
 //   phase 3  the workgroup copies the tokens' memory vectors: the output of the block is one
 //            contiguous run of bytes, so thread c moves 16-byte chunk c (dwordx4 load from the
 //            table row, dwordx4 store into mem). Eight lanes cover one 128-byte bf16 row, a
-//            wavefront writes 1 KiB of consecutive output per instruction, and UNROLL chunks
-//            per thread are in flight before the first store.
+//            wavefront writes 1 KiB of consecutive output per instruction, and all of a
+//            thread's chunks (up to kUnroll) are in flight before its first store.
+// The kernel is a chain of dependent memory round trips (token ids -> canon entry -> table
+// row -> store), and all workgroups of a launch are resident at once, so the chain's latency
+// is paid once per launch and is the part of the time that is not bandwidth: the constants
+// load off the chain, a null canon (identity map) takes one round trip out of it, and the
+// row copy keeps every load of a thread in flight together. The output is written with
+// non-temporal stores: it is consumed by the next kernel, and streaming it past the caches
+// leaves them to the table rows (hot n-grams repeat) instead of dirty lines to write back.
 // The row ids staged in LDS are what lets the copy run at full width: each output chunk is
 // one lane's register, so the concatenated vector needs no further LDS round trip.
 #include "me_common.h"
@@ -27,7 +36,7 @@ namespace me {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;
 
 enum Mode : int { kModeSeq = 0, kModePrev = 1, kModeIdx = 2 };
 
@@ -49,7 +58,7 @@ struct LookupArgs {
     const void *pos;
     int pos_i64;
     int64_t pos_bstride;
-    const int64_t *canon;
+    const int64_t *canon;  // nullable: identity map over [0, vocab)
     int64_t vocab;
     const int64_t *mults;
     int max_order;
@@ -74,11 +83,13 @@ __device__ __forceinline__ int64_t load_id(const void *p, int is64, int64_t i) {
                 : static_cast<int64_t>(static_cast<const int32_t *>(p)[i]);
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 template <int VEC>
 struct Chunk;
 template <>
 struct Chunk<16> {
-    using T = uint4;
+    using T = u32x4_t;
 };
 template <>
 struct Chunk<4> {
@@ -93,11 +104,7 @@ template <int MODE, int VEC>
 __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
     using V = typename Chunk<VEC>::T;
     __shared__ int64_t s_tok[64 * ME_MAX_ORDER];  // [tpb][max_order] hashed token values
-    __shared__ int64_t s_mult[ME_MAX_TABLES * ME_MAX_ORDER];
     __shared__ uint64_t s_src[kBlock];  // [tpb * n_tables] source row address, token-major
-    __shared__ uint64_t s_magic[ME_MAX_TABLES];
-    __shared__ uint32_t s_rows32[ME_MAX_TABLES];
-    __shared__ int32_t s_order[ME_MAX_TABLES];
 
     const int tid = threadIdx.x;
     const int nt = a.n_tables;
@@ -105,32 +112,48 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
     const int64_t g0 = static_cast<int64_t>(blockIdx.x) * a.tpb;
     const int ntok = static_cast<int>(min(static_cast<int64_t>(a.tpb), a.n - g0));
 
-    // ---- phase 0: per-table constants into LDS
-    if (MODE != kModeIdx) {
-        for (int e = tid; e < nt * mo; e += kBlock) s_mult[e] = a.mults[e];
-        if (tid < nt) {
-            s_magic[tid] = a.meta.magic[tid];
-            s_rows32[tid] = a.meta.rows32[tid];
-            s_order[tid] = a.meta.order[tid];
+    // ---- phase 0: this thread's (token, table) pair and its table constants, in registers;
+    // token index fastest so the [n_tables, n] row-id writes coalesce
+    const int wi = tid & (a.tpb - 1);
+    const int wk = tid >> a.tpb_shift;
+    const bool worker = tid < a.tpb * nt && wi < ntok;
+    uint64_t mult[ME_MAX_ORDER];
+    int order = 0;
+    uint64_t magic = 0, base = 0;
+    uint32_t rows32 = 0;
+    int64_t rows = 0, given = 0;
+    if (worker) {
+        base = a.meta.base[wk];
+        if (MODE == kModeIdx) {
+            rows = a.meta.rows[wk];
+            given = a.idx_in[wk * a.idx_stride + g0 + wi];
+        } else {
+            order = a.meta.order[wk];
+            magic = a.meta.magic[wk];
+            rows32 = a.meta.rows32[wk];
+#pragma unroll
+            for (int s = 0; s < ME_MAX_ORDER; ++s)
+                mult[s] = s < mo ? static_cast<uint64_t>(a.mults[wk * mo + s]) : 0ull;
         }
     }
 
-    // ---- phase 1: n-gram token values
+    // ---- phase 1: n-gram token values. The id load is issued from a clamped address before
+    // the window and document checks resolve, so its latency overlaps them.
     if (MODE == kModeSeq) {
+        const uint32_t seq_len = static_cast<uint32_t>(a.seq_len);
         for (int e = tid; e < ntok * mo; e += kBlock) {
             const int i = e / mo, s = e - i * mo;
             const int64_t g = g0 + i;
-            const int64_t t = g % a.seq_len;
-            bool ok = (t - s) >= 0;
-            if (ok && s > 0 && a.pos != nullptr) {
-                const int64_t b = g / a.seq_len;
-                ok = load_id(a.pos, a.pos_i64, b * a.pos_bstride + t) >= s;
-            }
+            const int64_t id_raw = load_id(a.ids, a.ids_i64, g - s >= 0 ? g - s : 0);
+            const uint32_t b = static_cast<uint32_t>(g) / seq_len;
+            const uint32_t t = static_cast<uint32_t>(g) - b * seq_len;
+            bool ok = static_cast<int>(t) >= s;
+            if (ok && s > 0 && a.pos != nullptr)
+                ok = load_id(a.pos, a.pos_i64, static_cast<int64_t>(b) * a.pos_bstride + t) >= s;
             int64_t v = a.pad_id;
             if (ok) {
-                int64_t id = load_id(a.ids, a.ids_i64, g - s);
-                id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
-                v = a.canon[id];
+                const int64_t id = id_raw < 0 ? 0 : (id_raw >= a.vocab ? a.vocab - 1 : id_raw);
+                v = a.canon != nullptr ? a.canon[id] : id;
             }
             s_tok[i * ME_MAX_ORDER + s] = v;
         }
@@ -141,52 +164,50 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
             int64_t v = a.pad_id;
             if (id >= 0) {
                 id = id >= a.vocab ? a.vocab - 1 : id;
-                v = a.canon[id];
+                v = a.canon != nullptr ? a.canon[id] : id;
             }
             s_tok[i * ME_MAX_ORDER + s] = v;
         }
     }
-    __syncthreads();
+    if (MODE != kModeIdx) __syncthreads();
 
-    // ---- phase 2: one thread per (token, table); token index fastest so idx writes coalesce
-    if (tid < a.tpb * nt) {
-        const int i = tid & (a.tpb - 1);
-        const int k = tid >> a.tpb_shift;
-        if (i < ntok) {
-            const int64_t g = g0 + i;
-            int64_t r;
-            bool valid = true;
-            if (MODE == kModeIdx) {
-                r = a.idx_in[k * a.idx_stride + g];
-                valid = r >= 0 && r < a.meta.rows[k];
-            } else {
-                uint64_t x = 0;
-                const int ord = s_order[k];
-                for (int s = 0; s < ord; ++s)
-                    x += static_cast<uint64_t>(s_tok[i * ME_MAX_ORDER + s]) *
-                         static_cast<uint64_t>(s_mult[k * mo + s]);
-                uint32_t h = floor_mod_prime(x);
-                const uint32_t d = s_rows32[k];
-                if (d != 0) h = fastmod_u32(h, s_magic[k], d);
-                r = h;
-                if (a.idx_out != nullptr) a.idx_out[k * a.n + g] = r;
-            }
-            if (a.mem != nullptr)
-                s_src[i * nt + k] =
-                    valid ? a.meta.base[k] + static_cast<uint64_t>(r) * a.row_bytes : 0ull;
+    // ---- phase 2: hash (or check the given row id), publish the source row address
+    if (worker) {
+        int64_t r;
+        bool valid = true;
+        if (MODE == kModeIdx) {
+            r = given;
+            valid = r >= 0 && r < rows;
+        } else {
+            uint64_t x = 0;
+#pragma unroll
+            for (int s = 0; s < ME_MAX_ORDER; ++s)
+                if (s < order) x += static_cast<uint64_t>(s_tok[wi * ME_MAX_ORDER + s]) * mult[s];
+            uint32_t h = floor_mod_prime(x);
+            if (rows32 != 0) h = fastmod_u32(h, magic, rows32);
+            r = h;
+            if (a.idx_out != nullptr) a.idx_out[wk * a.n + g0 + wi] = r;
         }
+        if (a.mem != nullptr)
+            s_src[wi * nt + wk] = valid ? base + static_cast<uint64_t>(r) * a.row_bytes : 0ull;
     }
     if (a.mem == nullptr) return;  // uniform: hash-only launch
     __syncthreads();
 
-    // ---- phase 3: copy the block's memory vectors, chunk c of the block's output run
+    // ---- phase 3: copy the block's memory vectors, chunk c of the block's output run. A
+    // thread's chunks are walked in an order rotated by the block index, so that at any moment
+    // the workgroups write different 4 KiB pieces of their runs instead of all writing the
+    // same piece (runs are equal-sized and adjacent).
     const int total = ntok * nt * a.cpr;
     uint8_t *dst = a.mem + static_cast<uint64_t>(g0) * nt * a.row_bytes;
     for (int c0 = tid; c0 < total; c0 += kBlock * kUnroll) {
+        const int steps = min(kUnroll, (total - (c0 - tid) + kBlock - 1) / kBlock);
+        const int rot = static_cast<int>(blockIdx.x % static_cast<unsigned>(steps));
         V v[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const int c = c0 + u * kBlock;
+            const int ur = u < steps ? (u + rot < steps ? u + rot : u + rot - steps) : u;
+            const int c = c0 + ur * kBlock;
             v[u] = V{};
             if (c < total) {
                 const int p = a.cpr_shift >= 0 ? (c >> a.cpr_shift) : (c / a.cpr);
@@ -198,8 +219,11 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const int c = c0 + u * kBlock;
-            if (c < total) *reinterpret_cast<V *>(dst + static_cast<uint64_t>(c) * VEC) = v[u];
+            const int ur = u < steps ? (u + rot < steps ? u + rot : u + rot - steps) : u;
+            const int c = c0 + ur * kBlock;
+            if (c < total)
+                __builtin_nontemporal_store(
+                    v[u], reinterpret_cast<V *>(dst + static_cast<uint64_t>(c) * VEC));
         }
     }
 }
@@ -283,7 +307,7 @@ int launch(const LookupArgs &a, int vec, hipStream_t stream, const char *what) {
 
 int common_hash_args(LookupArgs &a, const int64_t *canon, int64_t vocab, const int64_t *mults,
                      int64_t pad_id) {
-    ME_CHECK_ARG(canon != nullptr && mults != nullptr, "canon and mults must not be null");
+    ME_CHECK_ARG(mults != nullptr, "mults must not be null");
     ME_CHECK_ARG(vocab >= 1, "vocab must be positive");
     a.canon = canon;
     a.vocab = vocab;

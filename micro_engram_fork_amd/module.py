@@ -17,6 +17,8 @@ Differences from the reference, all deliberate:
     raises instead of silently detaching. Use torch.no_grad() / torch.inference_mode().
   * The "ple" gate keeps its parameters (so checkpoints load) but has no HIP kernel.
 """
+import weakref
+
 import torch
 import torch.nn as nn
 
@@ -109,6 +111,7 @@ class MicroEngram(nn.Module):
                               device="cpu") | 1
         self.register_buffer("mults", mults)
 
+        identity = canon is None
         if canon is None:
             canon = torch.arange(vocab_size)
         else:
@@ -116,6 +119,8 @@ class MicroEngram(nn.Module):
             if canon.shape != (vocab_size,):
                 raise ValueError(f"canon must have shape ({vocab_size},), got {tuple(canon.shape)}")
         self.register_buffer("canon", canon)
+        # identity_canon() state: (weakref to the buffer it was decided for, its version, result)
+        self._canon_state = (weakref.ref(self.canon), self.canon._version, True) if identity else None
 
     # ------------------------------------------------------------------ row shards (world = 1)
     def shard_rows(self, rank, world, device=None, dtype=None, requires_grad=True, empty=False,
@@ -178,26 +183,56 @@ class MicroEngram(nn.Module):
                                       unexpected_keys, error_msgs)
 
     # ------------------------------------------------------------------------------- hashing
+    def identity_canon(self):
+        """True while the canon buffer is the identity map, so the kernels can skip its read
+        (module.py:101-107 builds arange(vocab) when no map is given). Known without reading the
+        buffer while it is the same tensor at the same version (in-place writes, including
+        load_state_dict's copy, move the version); otherwise checked once on its device (one
+        host read). Writes through .data bypass the version counter and are not seen."""
+        c = self.canon
+        st = self._canon_state
+        if st is not None and st[0]() is c and st[1] == c._version:
+            return st[2]
+        if torch.compiler.is_compiling():
+            return False
+        ident = bool(torch.equal(c, torch.arange(c.numel(), device=c.device, dtype=c.dtype)))
+        self._canon_state = (weakref.ref(c), c._version, ident)
+        return ident
+
+    def __getstate__(self):
+        state = self.__dict__.copy()
+        state["_canon_state"] = None  # a weakref does not copy; the copy decides again
+        return state
+
+    def _apply(self, fn, *args, **kwargs):
+        # .to() / .cuda() give the buffer a new tensor with the same values: keep the decision
+        st = self._canon_state
+        known = st is not None and st[0]() is self.canon and st[1] == self.canon._version
+        out = super()._apply(fn, *args, **kwargs)
+        if known:
+            self._canon_state = (weakref.ref(self.canon), self.canon._version, st[2])
+        return out
+
     def _hash_consts(self, device):
         canon = self.canon if self.canon.device == device else self.canon.to(device)
         mults = self.mults if self.mults.device == device else self.mults.to(device)
-        return canon, mults
+        return canon, mults, self.identity_canon()
 
     def hash_ids(self, input_ids, position_ids=None):
         """Row ids of the n-grams ending at every position: list of n_tables LongTensors shaped
         like input_ids [B, T] (module.py:183-205)."""
-        canon, mults = self._hash_consts(input_ids.device)
+        canon, mults, ident = self._hash_consts(input_ids.device)
         pos = position_ids.to(input_ids.device) if position_ids is not None else None
         idx = ops.hash_ids(input_ids, pos, canon, mults, self._table_orders, self.table_rows,
-                           int(self.pad_id))
+                           int(self.pad_id), ident)
         return list(idx.unbind(0))
 
     def hash_prev(self, ids):
         """Row ids from [N, W] ids of each token and its predecessors, -1 where missing: list of
         n_tables LongTensors [N] (module.py:207-226)."""
-        canon, mults = self._hash_consts(ids.device)
+        canon, mults, ident = self._hash_consts(ids.device)
         idx = ops.hash_prev(ids, canon, mults, self._table_orders, self.table_rows,
-                            int(self.pad_id))
+                            int(self.pad_id), ident)
         return list(idx.unbind(0))
 
     # -------------------------------------------------------------------------------- lookup
@@ -280,10 +315,10 @@ class MicroEngram(nn.Module):
         lookup + cat (module.py:183-205, 146-154, 233) as one fused kernel."""
         device = device or input_ids.device
         input_ids = input_ids.to(device)
-        canon, mults = self._hash_consts(device)
+        canon, mults, ident = self._hash_consts(device)
         pos = position_ids.to(device) if position_ids is not None else None
         return ops.hash_gather(input_ids, pos, canon, mults, self._table_orders, self.table_rows,
-                               int(self.pad_id), self._table_weights(), False)[0]
+                               int(self.pad_id), self._table_weights(), False, ident)[0]
 
     def gate_residual(self, hidden, mem, keep=None):
         """hidden + the gated projection of the memory vectors `mem` (module.py:239-261)."""

@@ -73,6 +73,11 @@ def _ids2d(input_ids):
     return ids.contiguous()
 
 
+def _canon_ptr(canon, identity):
+    """The canon map's address, or NULL for the identity map (the kernels then skip the read)."""
+    return None if identity else canon.data_ptr()
+
+
 def _table_args(table_orders, table_rows):
     return len(table_orders), i32_array(list(table_orders)), i64_array(list(table_rows))
 
@@ -80,8 +85,9 @@ def _table_args(table_orders, table_rows):
 @torch.library.custom_op("micro_engram_amd::hash_ids", mutates_args=())
 def hash_ids(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], canon: torch.Tensor,
              mults: torch.Tensor, table_orders: List[int], table_rows: List[int],
-             pad_id: int) -> torch.Tensor:
-    """Row ids int64 [n_tables, B, T] (micro_engram/module.py:183-205)."""
+             pad_id: int, identity_canon: bool = False) -> torch.Tensor:
+    """Row ids int64 [n_tables, B, T] (micro_engram/module.py:183-205). identity_canon: the
+    caller guarantees canon[i] == i, so the kernel skips the canon read."""
     dev = require_gpu(input_ids, position_ids, canon, mults)
     ids = _ids2d(input_ids)
     B, T = ids.shape
@@ -89,13 +95,14 @@ def hash_ids(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], cano
     nt, orders, rows = _table_args(table_orders, table_rows)
     out = torch.empty((nt, B, T), dtype=torch.int64, device=dev)
     call("me_hash_ngrams", ids.data_ptr(), dtype_code(ids), B, T, _p(pos),
-         dtype_code(pos) if pos is not None else 0, pstride, canon.data_ptr(), canon.numel(),
-         mults.data_ptr(), mults.shape[1], nt, orders, rows, pad_id, out.data_ptr(), stream_of(dev))
+         dtype_code(pos) if pos is not None else 0, pstride, _canon_ptr(canon, identity_canon),
+         canon.numel(), mults.data_ptr(), mults.shape[1], nt, orders, rows, pad_id, out.data_ptr(),
+         stream_of(dev))
     return out
 
 
 @hash_ids.register_fake
-def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id):
+def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id, identity_canon=False):
     return input_ids.new_empty((len(table_orders), *input_ids.shape), dtype=torch.int64)
 
 
@@ -111,7 +118,8 @@ def _prev_ids(ids):
 
 @torch.library.custom_op("micro_engram_amd::hash_prev", mutates_args=())
 def hash_prev(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
-              table_orders: List[int], table_rows: List[int], pad_id: int) -> torch.Tensor:
+              table_orders: List[int], table_rows: List[int], pad_id: int,
+              identity_canon: bool = False) -> torch.Tensor:
     """Row ids int64 [n_tables, N] from [N, W] predecessor ids (micro_engram/module.py:207-226)."""
     dev = require_gpu(ids, canon, mults)
     ids = _prev_ids(ids)
@@ -119,13 +127,13 @@ def hash_prev(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
     nt, orders, rows = _table_args(table_orders, table_rows)
     out = torch.empty((nt, N), dtype=torch.int64, device=dev)
     call("me_hash_prev", ids.data_ptr(), dtype_code(ids), N, W, ids.stride(0) if N else W,
-         canon.data_ptr(), canon.numel(), mults.data_ptr(), mults.shape[1], nt, orders, rows,
-         pad_id, out.data_ptr(), stream_of(dev))
+         _canon_ptr(canon, identity_canon), canon.numel(), mults.data_ptr(), mults.shape[1], nt,
+         orders, rows, pad_id, out.data_ptr(), stream_of(dev))
     return out
 
 
 @hash_prev.register_fake
-def _(ids, canon, mults, table_orders, table_rows, pad_id):
+def _(ids, canon, mults, table_orders, table_rows, pad_id, identity_canon=False):
     return ids.new_empty((len(table_orders), ids.shape[0]), dtype=torch.int64)
 
 
@@ -166,7 +174,8 @@ def _(idx, tables):
 @torch.library.custom_op("micro_engram_amd::hash_gather", mutates_args=())
 def hash_gather(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], canon: torch.Tensor,
                 mults: torch.Tensor, table_orders: List[int], table_rows: List[int], pad_id: int,
-                tables: List[torch.Tensor], with_idx: bool) -> List[torch.Tensor]:
+                tables: List[torch.Tensor], with_idx: bool,
+                identity_canon: bool = False) -> List[torch.Tensor]:
     """[mem [B*T, n_tables*D]] or [mem, idx [n_tables, B, T]]: hash_ids + lookup + cat in one
     kernel (module.py:263-265)."""
     dev = require_gpu(input_ids, position_ids, canon, mults, *tables)
@@ -178,14 +187,15 @@ def hash_gather(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], c
     mem = torch.empty((B * T, nt * dim), dtype=tables[0].dtype, device=dev)
     idx = torch.empty((nt, B, T), dtype=torch.int64, device=dev) if with_idx else None
     call("me_hash_gather", ids.data_ptr(), dtype_code(ids), B, T, _p(pos),
-         dtype_code(pos) if pos is not None else 0, pstride, canon.data_ptr(), canon.numel(),
-         mults.data_ptr(), mults.shape[1], nt, orders, rows, pad_id, ptrs, dim,
+         dtype_code(pos) if pos is not None else 0, pstride, _canon_ptr(canon, identity_canon),
+         canon.numel(), mults.data_ptr(), mults.shape[1], nt, orders, rows, pad_id, ptrs, dim,
          dtype_code(tables[0]), mem.data_ptr(), _p(idx), stream_of(dev))
     return [mem, idx] if with_idx else [mem]
 
 
 @hash_gather.register_fake
-def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id, tables, with_idx):
+def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id, tables, with_idx,
+      identity_canon=False):
     n = input_ids.shape[0] * input_ids.shape[1]
     mem = tables[0].new_empty((n, len(tables) * tables[0].shape[1]))
     if with_idx:
@@ -196,7 +206,8 @@ def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id, t
 @torch.library.custom_op("micro_engram_amd::hash_prev_gather", mutates_args=())
 def hash_prev_gather(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
                      table_orders: List[int], table_rows: List[int], pad_id: int,
-                     tables: List[torch.Tensor], with_idx: bool) -> List[torch.Tensor]:
+                     tables: List[torch.Tensor], with_idx: bool,
+                     identity_canon: bool = False) -> List[torch.Tensor]:
     """[mem [N, n_tables*D]] or [mem, idx [n_tables, N]]: hash_prev + lookup in one kernel."""
     dev = require_gpu(ids, canon, mults, *tables)
     ids = _prev_ids(ids)
@@ -206,13 +217,14 @@ def hash_prev_gather(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor
     mem = torch.empty((N, nt * dim), dtype=tables[0].dtype, device=dev)
     idx = torch.empty((nt, N), dtype=torch.int64, device=dev) if with_idx else None
     call("me_hash_prev_gather", ids.data_ptr(), dtype_code(ids), N, W, ids.stride(0) if N else W,
-         canon.data_ptr(), canon.numel(), mults.data_ptr(), mults.shape[1], nt, orders, rows,
-         pad_id, ptrs, dim, dtype_code(tables[0]), mem.data_ptr(), _p(idx), stream_of(dev))
+         _canon_ptr(canon, identity_canon), canon.numel(), mults.data_ptr(), mults.shape[1], nt,
+         orders, rows, pad_id, ptrs, dim, dtype_code(tables[0]), mem.data_ptr(), _p(idx),
+         stream_of(dev))
     return [mem, idx] if with_idx else [mem]
 
 
 @hash_prev_gather.register_fake
-def _(ids, canon, mults, table_orders, table_rows, pad_id, tables, with_idx):
+def _(ids, canon, mults, table_orders, table_rows, pad_id, tables, with_idx, identity_canon=False):
     mem = tables[0].new_empty((ids.shape[0], len(tables) * tables[0].shape[1]))
     if with_idx:
         return [mem, ids.new_empty((len(tables), ids.shape[0]), dtype=torch.int64)]

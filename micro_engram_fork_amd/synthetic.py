@@ -123,14 +123,20 @@ def tiny_inputs(seed=0, device="cpu"):
     return ids, pos, hidden
 
 
-def prefill_inputs(seed=0, batch=1, seq=8192, device="cpu", dim=GEMMA_DIM, dtype=torch.bfloat16):
-    """Zipf(1.1) ids over the gemma vocab, packed documents; hidden ~N(0,1)."""
+def prefill_ids(seed=0, batch=1, seq=8192, device="cpu"):
+    """Zipf(1.1) ids over the gemma vocab [batch, seq] and the positions of packed documents."""
     rng = np.random.Generator(np.random.PCG64(seed))
     ids = np.stack([zipf_ids(rng, seq, GEMMA_VOCAB) for _ in range(batch)])
     pos = np.stack([packed_positions(rng, seq) for _ in range(batch)])
+    return torch.from_numpy(ids).to(device), torch.from_numpy(pos).to(device)
+
+
+def prefill_inputs(seed=0, batch=1, seq=8192, device="cpu", dim=GEMMA_DIM, dtype=torch.bfloat16):
+    """prefill_ids plus hidden ~N(0,1) [batch, seq, dim]."""
+    ids, pos = prefill_ids(seed, batch, seq, device)
     gen = torch.Generator().manual_seed(seed + 1)
     hidden = torch.randn(batch, seq, dim, generator=gen).to(dtype)
-    return (torch.from_numpy(ids).to(device), torch.from_numpy(pos).to(device), hidden.to(device))
+    return ids, pos, hidden.to(device)
 
 
 def decode_inputs(seed=0, n_seq=256, max_order=4, device="cpu", dim=GEMMA_DIM,

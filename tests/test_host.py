@@ -115,3 +115,29 @@ def test_bad_gate_and_canon_rejected():
         MicroEngram(model_dim=8, gate="bogus")
     with pytest.raises(ValueError):
         MicroEngram(model_dim=8, table_size=17, vocab_size=50, canon=torch.arange(49))
+
+
+def test_identity_canon_tracking():
+    # the identity decision follows the buffer: known at construction, carried over .to(), lost
+    # on any in-place write or replacement, re-decided from the values (load_state_dict copies)
+    import copy
+
+    eng = MicroEngram(64, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3), vocab_size=50)
+    assert eng.identity_canon()
+    eng = eng.to(torch.float64)
+    assert eng._canon_state is not None and eng.identity_canon()
+    eng.canon[3] = 7
+    assert not eng.identity_canon()
+    eng.canon[3] = 3
+    assert eng.identity_canon()
+    sd = eng.state_dict()
+    sd["canon"] = torch.arange(50).flip(0)
+    eng.load_state_dict(sd)
+    assert not eng.identity_canon()
+    merged = MicroEngram(64, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3), vocab_size=50,
+                         canon=torch.arange(50))
+    assert merged._canon_state is None and merged.identity_canon()
+    clone = copy.deepcopy(eng)
+    assert not clone.identity_canon()
+    eng.canon = torch.arange(50)
+    assert eng.identity_canon()
