@@ -17,6 +17,9 @@ all inputs already in HBM. Prints one JSON line:
                 reference and the known-size kernel that calibrates the HBM byte counters
   roofline_gate the K/V projection kernels: 4 * M * d FLOP per token / their mean duration
                 (graph replay), against 2.5 PFLOP/s dense bf16
+  roofline_update  the training-side sparse update of a batch of this shape (dedup of the
+                196,608 lookups + row-wise Adam with stochastic rounding on the touched rows),
+                algorithmic bytes / duration over 16 distinct batches, against 8 TB/s
   cpu_baseline  the oracle's torch-CPU forward on a token sample of the same batch
 """
 import argparse
@@ -27,6 +30,8 @@ import time
 
 import numpy as np
 import torch
+
+from micro_engram_fork_amd import ops, synthetic
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -57,6 +62,39 @@ def gather_bytes_per_token(eng, esize, canon_read):
     identity (8 bytes each)."""
     n_t = len(eng.table_rows)
     return n_t * eng.engram_dim * esize * 2 + 16 + (8 if canon_read else 0)
+
+
+def update_batches(eng, dev, n_batches):
+    """The training-side sparse update of n prefill batches of the workload's shape: each
+    batch's 196,608 (token, table) lookups with fp32 gradients N(0, 1e-3), as keys into the
+    concatenated tables (token-major, the order of the row lookup's backward)."""
+    offs = [0]
+    for r in eng.table_rows:
+        offs.append(offs[-1] + r)
+    off_t = torch.tensor(offs[:-1], device=dev)[:, None]
+    out = []
+    for s in range(n_batches):
+        ids, pos = synthetic.prefill_ids(seed=s, device=dev)
+        idx = torch.stack(eng.hash_ids(ids, pos)).reshape(len(eng.tables), -1)
+        keys = (idx + off_t).t().reshape(-1).contiguous()
+        grads = synthetic.lookup_grads(keys.numel(), eng.engram_dim, seed=s, device=dev)
+        uniq, _inv, count, gsum = ops.dedup(keys, offs[-1], grads)
+        n_uniq = int(count.item())
+        bounds = torch.searchsorted(uniq[:n_uniq], torch.tensor(offs, device=dev)).tolist()
+        rows = [uniq[bounds[k]:bounds[k + 1]] - offs[k] for k in range(len(eng.tables))]
+        sums = [gsum[bounds[k]:bounds[k + 1]] for k in range(len(eng.tables))]
+        out.append((keys, grads, rows, sums, n_uniq))
+    return out, offs[-1]
+
+
+def update_bytes(n_lookups, n_uniq, dim, esize):
+    """Algorithmic bytes of one sparse update. Dedup: read the int64 keys and fp32 gradient
+    rows; write the unique keys, the int64 inverse and the summed fp32 rows. Row-wise Adam per
+    unique row: weight and first moment read and written (esize each), the fp32 second moment
+    read and written, the summed gradient and the row id read (784 B for 64 bf16)."""
+    dedup = n_lookups * (8 + 4 * dim) + n_uniq * (8 + 4 * dim) + n_lookups * 8
+    adam = n_uniq * (4 * dim * esize + 8 + 4 * dim + 8)
+    return dedup, adam
 
 
 def cpu_baseline(eng, ids, pos, hidden, target_s):
@@ -108,8 +146,6 @@ def main():
         print(f"bench.py measures one GPU: the engram path here has no multi-GPU mode "
               f"(asked for --gpus {args.gpus}). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    from micro_engram_fork_amd import synthetic
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     eng = synthetic.build_engram("gemma", dev, seed=0).eval()
@@ -167,6 +203,28 @@ def main():
         del cycle, gathers
         mem = eng.hashed_memory(ids, pos, dev)
         gate_ms = replay_ms([lambda: eng.gate_residual(hidden, mem)], 10)
+
+        # The sparse update (dedup + row-wise Adam with stochastic rounding) of the same
+        # batch shape, also over a cycle of distinct batches; it writes the tables, so it runs
+        # after the forward measurements.
+        ubatches, key_bound = update_batches(eng, dev, GATHER_CYCLE)
+        tables = [t.weight.detach() for t in eng.tables]
+        exp_avgs = [torch.zeros_like(t) for t in tables]
+        exp_avg_sqs = [torch.zeros(t.shape[0], device=dev) for t in tables]
+        streams = list(range(len(tables)))
+
+        def adam_of(rows, sums):
+            return lambda: ops.sparse_adam(
+                tables, exp_avgs, exp_avg_sqs, rows, sums, [1] * len(tables), streams, lr=5e-3,
+                betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, rowwise=True, lazy=True,
+                stochastic_rounding=True, seed=2024)
+
+        dedup_ms = replay_ms([(lambda k=k, g=g: ops.dedup(k, key_bound, g))
+                              for k, g, _, _, _ in ubatches], 2) / len(ubatches)
+        adam_ms = replay_ms([adam_of(r, g) for _, _, r, g, _ in ubatches], 2) / len(ubatches)
+        n_lookups = ubatches[0][0].numel()
+        n_uniq = float(np.mean([u[4] for u in ubatches]))
+        del ubatches, exp_avgs, exp_avg_sqs
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         copy_ms = replay_ms([lambda: dst.copy_(src)], 5)
@@ -182,6 +240,8 @@ def main():
     gate_flop = 4.0 * M * d * T
     gate_tflops = gate_flop / (gate_ms * 1e-3) / 1e12
 
+    dedup_b, adam_b = update_bytes(n_lookups, n_uniq, eng.engram_dim, esize)
+    update_gbs = (dedup_b + adam_b) / ((dedup_ms + adam_ms) * 1e-3) / 1e9
     result = {
         "metric": "Engram fwd tokens/sec @8192-token prefill on 1 GPU; gather HBM GB/s vs peak",
         "value": T * args.steps / wall,
@@ -224,6 +284,21 @@ def main():
             "frac": gate_tflops / BF16_PEAK_TFLOPS,
             "flop_per_launch": gate_flop,
             "mean_ms": gate_ms,
+        },
+        "roofline_update": {
+            "kernel": "sparse update: dedup (radix sort + segment sums) + row-wise Adam with "
+                      "stochastic rounding",
+            "bound": "hbm",
+            "achieved": update_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": update_gbs / HBM_PEAK_GBS,
+            "lookups": n_lookups,
+            "unique_rows_mean": n_uniq,
+            "dedup_ms": dedup_ms,
+            "dedup_gbs": dedup_b / (dedup_ms * 1e-3) / 1e9,
+            "adam_ms": adam_ms,
+            "adam_gbs": adam_b / (adam_ms * 1e-3) / 1e9,
         },
         "cpu_baseline": None,
     }
