@@ -28,13 +28,14 @@ constexpr int kThreads = 256;
 constexpr int kItems = 8;                        // elements per thread per tile
 constexpr int kTile = kThreads * kItems;         // 2048 elements per sort block
 constexpr int kBins = 256;                       // 8-bit digits
-constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ uint64_t lanes_below(int lane) { return (1ull << lane) - 1ull; }
 
 // ---- radix sort -----------------------------------------------------------------------------
+// hist[digit * stride + tile]: row `digit` holds that digit's count in every tile; rows are
+// padded to a multiple of 4 tiles (zeros) so a row reads as 16-byte words.
 __global__ __launch_bounds__(kThreads) void rs_hist(const uint64_t *keys, int64_t n, int shift,
-                                                    uint32_t *hist, int nblocks) {
+                                                    uint32_t *hist, int nblocks, int stride) {
     __shared__ uint32_t s[kBins];
     const int tid = threadIdx.x;
     s[tid] = 0;
@@ -46,44 +47,61 @@ __global__ __launch_bounds__(kThreads) void rs_hist(const uint64_t *keys, int64_
         if (idx < n) atomicAdd(&s[(keys[idx] >> shift) & (kBins - 1)], 1u);
     }
     __syncthreads();
-    hist[static_cast<int64_t>(tid) * nblocks + blockIdx.x] = s[tid];
+    hist[static_cast<int64_t>(tid) * stride + blockIdx.x] = s[tid];
+    if (blockIdx.x == 0)
+        for (int b = nblocks; b < stride; ++b) hist[static_cast<int64_t>(tid) * stride + b] = 0u;
 }
 
 // Exclusive prefix sum of v[0..total) in place, one workgroup. If total_out is given, the sum
 // of all entries is written there too.
-__global__ __launch_bounds__(kScanThreads) void scan_exclusive(uint32_t *v, int64_t total,
-                                                               int64_t *total_out) {
-    __shared__ uint32_t s[kScanThreads];
-    const int tid = threadIdx.x;
-    const int64_t per = (total + kScanThreads - 1) / kScanThreads;
-    const int64_t b = tid * per, e = min(total, b + per);
-    uint32_t sum = 0;
-    for (int64_t i = b; i < e; ++i) sum += v[i];
-    s[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < kScanThreads; off <<= 1) {  // Hillis-Steele inclusive scan
-        const uint32_t t = tid >= off ? s[tid - off] : 0u;
-        __syncthreads();
-        s[tid] += t;
-        __syncthreads();
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t x, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
     }
-    uint32_t run = s[tid] - sum;  // exclusive prefix of this thread's chunk
-    for (int64_t i = b; i < e; ++i) {
-        const uint32_t x = v[i];
-        v[i] = run;
-        run += x;
-    }
-    if (total_out != nullptr && tid == kScanThreads - 1) *total_out = s[tid];
+    return x;
 }
 
+// Scatter of one tile. Its output base for digit d = (all keys with a smaller digit) + (keys
+// with digit d in earlier tiles): thread d reads row d of the histogram as 16-byte words,
+// summing the earlier tiles and all tiles, and a scan of the 256 totals across the workgroup
+// orders the digits. Every tile derives its bases itself, so a pass is two launches.
 __global__ __launch_bounds__(kThreads) void rs_scatter(const uint64_t *keys_in, const uint32_t *pos_in,
                                                        uint64_t *keys_out, uint32_t *pos_out,
                                                        int64_t n, int shift, const uint32_t *hist,
-                                                       int nblocks) {
+                                                       int stride) {
     __shared__ uint32_t s_base[kBins];
     __shared__ uint32_t s_wcnt[kThreads / 64][kBins];
+    __shared__ uint32_t s_wtot[kThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    s_base[tid] = hist[static_cast<int64_t>(tid) * nblocks + blockIdx.x];
+    {
+        static_assert(kThreads == kBins, "one thread per digit");
+        const uint4 *row = reinterpret_cast<const uint4 *>(hist + static_cast<int64_t>(tid) * stride);
+        const int words = stride / 4, me = static_cast<int>(blockIdx.x);
+        uint32_t mine = 0, tot = 0;
+        for (int q0 = 0; q0 < words; q0 += 8) {
+            uint4 x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = q0 + u < words ? row[q0 + u] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int t0 = (q0 + u) * 4;
+                const uint32_t c[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    tot += c[e];
+                    if (t0 + e < me) mine += c[e];
+                }
+            }
+        }
+        const uint32_t incl = wave_inclusive_scan(tot, lane);
+        if (lane == 63) s_wtot[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0;
+        for (int w = 0; w < wave; ++w) before += s_wtot[w];
+        s_base[tid] = before + incl - tot + mine;
+    }
     const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
     for (int i = 0; i < kItems; ++i) {
         const int64_t idx = base + i * kThreads + tid;
@@ -145,11 +163,30 @@ __global__ __launch_bounds__(kThreads) void seg_count(const uint64_t *skeys, int
 }
 
 __global__ __launch_bounds__(kThreads) void seg_write(const uint64_t *skeys, const uint32_t *spos,
-                                                      int64_t n, const uint32_t *block_base,
-                                                      int64_t *uniq, int64_t *inv,
-                                                      uint32_t *seg_start) {
+                                                      int64_t n, const uint32_t *block_heads,
+                                                      int nblocks, int64_t *uniq, int64_t *inv,
+                                                      uint32_t *seg_start, uint32_t *seg_pos,
+                                                      int64_t *count) {
     __shared__ uint32_t s[kThreads];
-    const int tid = threadIdx.x;
+    __shared__ uint32_t s_before[kThreads / 64], s_all[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {   // heads in the tiles before this one (and in all tiles, for the count)
+        uint32_t before = 0, all = 0;
+        for (int b = tid; b < nblocks; b += kThreads) {
+            const uint32_t c = block_heads[b];
+            all += c;
+            if (b < static_cast<int>(blockIdx.x)) before += c;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            before += __shfl_xor(before, off, 64);
+            all += __shfl_xor(all, off, 64);
+        }
+        if (lane == 0) {
+            s_before[wave] = before;
+            s_all[wave] = all;
+        }
+    }
     const int64_t b = static_cast<int64_t>(blockIdx.x) * kTile + static_cast<int64_t>(tid) * kItems;
     uint32_t c = 0;
     for (int i = 0; i < kItems; ++i)
@@ -162,14 +199,22 @@ __global__ __launch_bounds__(kThreads) void seg_write(const uint64_t *skeys, con
         s[tid] += t;
         __syncthreads();
     }
+    uint32_t tile_base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        tile_base += s_before[w];
+        total += s_all[w];
+    }
+    if (blockIdx.x == 0 && tid == 0) *count = total;
     // heads before this thread's first element, over the whole array
-    uint32_t heads = block_base[blockIdx.x] + s[tid] - c;
+    uint32_t heads = tile_base + s[tid] - c;
     for (int i = 0; i < kItems; ++i) {
         const int64_t idx = b + i;
         if (idx >= n) break;
         if (is_head(skeys, idx)) {
             uniq[heads] = static_cast<int64_t>(skeys[idx]);
             seg_start[heads] = static_cast<uint32_t>(idx);
+            seg_pos[heads] = spos[idx];  // the segment's first row, one load less for the sums
             ++heads;
         }
         inv[spos[idx]] = static_cast<int64_t>(heads) - 1;
@@ -180,36 +225,64 @@ __global__ __launch_bounds__(kThreads) void seg_write(const uint64_t *skeys, con
 __global__ void write_zero_count(int64_t *count) { *count = 0; }
 
 // One thread per (segment, run of kCols columns): the segment's gradient rows summed in sorted
-// (= original) order, starting from +0.0 like zeros().index_add_().
+// (= original) order, starting from +0.0 like zeros().index_add_(). The segment's bounds, its
+// first row and the segment count are independent loads; rows after the first are fetched four
+// at a time and added in order.
+__device__ __forceinline__ void load_cols(const float *p, float (&x)[4]) {
+    const float4 v = *reinterpret_cast<const float4 *>(p);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+}
+__device__ __forceinline__ void load_cols(const uint16_t *p, float (&x)[4]) {
+    const uint2 v = *reinterpret_cast<const uint2 *>(p);
+    x[0] = bf16_bits_to_float(static_cast<uint16_t>(v.x));
+    x[1] = bf16_bits_to_float(static_cast<uint16_t>(v.x >> 16));
+    x[2] = bf16_bits_to_float(static_cast<uint16_t>(v.y));
+    x[3] = bf16_bits_to_float(static_cast<uint16_t>(v.y >> 16));
+}
+__device__ __forceinline__ void load_cols(const float *p, float (&x)[1]) { x[0] = *p; }
+__device__ __forceinline__ void load_cols(const uint16_t *p, float (&x)[1]) {
+    x[0] = bf16_bits_to_float(*p);
+}
+
 template <typename G, int kCols>
-__global__ __launch_bounds__(kThreads) void seg_sum(const G *grads, int dim, const uint32_t *spos,
-                                                    const uint32_t *seg_start,
-                                                    const int64_t *count, int64_t max_segs,
+__global__ __launch_bounds__(kThreads) void seg_sum(const G *grads, uint32_t dim, const uint32_t *spos,
+                                                    const uint32_t *seg_start, const uint32_t *seg_pos,
+                                                    const int64_t *count, uint32_t max_segs,
                                                     float *gsum) {
-    const int runs = dim / kCols;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    const int64_t seg = t / runs;
-    if (seg >= max_segs || seg >= *count) return;
-    const int c0 = static_cast<int>(t - seg * runs) * kCols;
-    float acc[kCols];
+    const uint32_t runs = dim / kCols;
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t seg = t / runs;
+    if (seg >= max_segs) return;
+    const uint32_t c0 = (t - seg * runs) * kCols;
+    const uint32_t lo = seg_start[seg], hi = seg_start[seg + 1], first = seg_pos[seg];
+    if (static_cast<int64_t>(seg) >= *count) return;
+    float acc[kCols], x[kCols];
+    load_cols(grads + static_cast<uint64_t>(first) * dim + c0, x);
 #pragma unroll
-    for (int c = 0; c < kCols; ++c) acc[c] = 0.f;
-    const uint32_t e = seg_start[seg + 1];
-    for (uint32_t i = seg_start[seg]; i < e; ++i) {
-        const G *row = grads + static_cast<int64_t>(spos[i]) * dim + c0;
+    for (int c = 0; c < kCols; ++c) acc[c] = 0.f + x[c];
+    uint32_t i = lo + 1;
+    for (; i + 4 <= hi; i += 4) {
+        uint32_t q[4];
+        float y[4][kCols];
 #pragma unroll
-        for (int c = 0; c < kCols; ++c) {
-            float g;
-            if constexpr (sizeof(G) == 2)
-                g = bf16_bits_to_float(row[c]);
-            else
-                g = row[c];
-            acc[c] = acc[c] + g;
-        }
+        for (int u = 0; u < 4; ++u) q[u] = spos[i + u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_cols(grads + static_cast<uint64_t>(q[u]) * dim + c0, y[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + y[u][c];
     }
-    float *out = gsum + seg * dim + c0;
+    for (; i < hi; ++i) {
+        load_cols(grads + static_cast<uint64_t>(spos[i]) * dim + c0, x);
 #pragma unroll
-    for (int c = 0; c < kCols; ++c) out[c] = acc[c];
+        for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + x[c];
+    }
+    float *out = gsum + static_cast<uint64_t>(seg) * dim + c0;
+    if constexpr (kCols == 4)
+        *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    else
+        out[0] = acc[0];
 }
 
 // ---- squared norm ---------------------------------------------------------------------------
@@ -393,6 +466,136 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
     if (a.rowwise && lane == 0) reinterpret_cast<float *>(t.exp_avg_sq)[row] = v_row;
 }
 
+// Four consecutive columns c0..c0+3 (c0 % 4 == 0) share one Philox call: the same noise
+// sr_noise gives each of them (word (col >> 1) & 3, half col & 1 of the call for col >> 3).
+__device__ __forceinline__ void sr_noise4(uint64_t seed, uint32_t step, uint32_t table,
+                                          uint64_t row, uint32_t c0, uint32_t which,
+                                          uint32_t (&nz)[4]) {
+    const uint4 ctr = make_uint4(static_cast<uint32_t>(row), static_cast<uint32_t>(row >> 32), step,
+                                 (table << 16) | (which << 14) | (c0 >> 3));
+    const uint4 w = philox4x32_10(ctr, make_uint2(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)));
+    const bool low = ((c0 >> 1) & 3) == 0;
+    const uint32_t wa = low ? w.x : w.z, wb = low ? w.y : w.w;
+    nz[0] = wa & 0xffffu;
+    nz[1] = wa >> 16;
+    nz[2] = wb & 0xffffu;
+    nz[3] = wb >> 16;
+}
+
+__device__ __forceinline__ void load4(const uint8_t *base, int bf16, int64_t e0, float (&x)[4]) {
+    if (bf16) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(base + e0 * 2);
+        x[0] = bf16_bits_to_float(static_cast<uint16_t>(v.x));
+        x[1] = bf16_bits_to_float(static_cast<uint16_t>(v.x >> 16));
+        x[2] = bf16_bits_to_float(static_cast<uint16_t>(v.y));
+        x[3] = bf16_bits_to_float(static_cast<uint16_t>(v.y >> 16));
+    } else {
+        const float4 v = *reinterpret_cast<const float4 *>(base + e0 * 4);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    }
+}
+
+__device__ __forceinline__ void store4(uint8_t *base, int bf16, int64_t e0, const float (&x)[4],
+                                       int sr, const uint32_t (&nz)[4]) {
+    if (bf16) {
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            h[e] = sr ? stochastic_bf16_bits(x[e], nz[e]) : float_to_bf16_bits_rne(x[e]);
+        *reinterpret_cast<uint2 *>(base + e0 * 2) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    } else {
+        *reinterpret_cast<float4 *>(base + e0 * 4) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+}
+
+// LPR lanes per touched row, four columns per lane (dim = 4 * LPR), 64 / LPR rows per wave:
+// the same update as adam_rows with vector loads, one Philox call per lane per rounded array,
+// and the launch's table list staged in LDS (rows of one wave may belong to different tables).
+template <int LPR>
+__global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
+    constexpr int kRowsPerWave = 64 / LPR;
+    constexpr int kRowsPerBlock = kRowsPerWave * (kThreads / 64);
+    constexpr int D = 4 * LPR;
+    __shared__ AdamTable s_t[kAdamTables];
+    const int tid = threadIdx.x;
+    {
+        static_assert(sizeof(AdamTable) % 8 == 0, "table record copied as 8-byte words");
+        const uint64_t *src = reinterpret_cast<const uint64_t *>(a.t);
+        uint64_t *dst = reinterpret_cast<uint64_t *>(s_t);
+        const int words = a.n_tables * static_cast<int>(sizeof(AdamTable) / 8);
+        for (int w = tid; w < words; w += kThreads) dst[w] = src[w];
+    }
+    __syncthreads();
+    const int lane = tid & 63;
+    const int sub = lane & (LPR - 1);
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (tid >> 6) * kRowsPerWave +
+                         lane / LPR;
+    if (slot >= a.total) return;  // whole rows: the lanes of one row share the slot
+    int lo = 0, hi = a.n_tables - 1;  // last table whose first slot is <= slot
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_t[mid].first <= slot) lo = mid; else hi = mid - 1;
+    }
+    const AdamTable &t = s_t[lo];
+    const int c0 = 4 * sub;
+    const int64_t i = slot - t.first;
+    const int64_t row = t.rows[i];
+    float g[4];
+    load4(reinterpret_cast<const uint8_t *>(t.grads), 0, i * D + c0, g);
+    float coef = 1.f;  // gradient clipping (rows.py:224-231): min(max_norm / (norm + 1e-6), 1)
+    if (a.sumsq != nullptr) coef = fminf(a.max_norm / (sqrtf(*a.sumsq) + 1e-6f), 1.0f);
+    bool any = false;
+    float gsq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (a.sumsq != nullptr) g[e] *= coef;
+        any |= g[e] != 0.f;
+        gsq += g[e] * g[e];
+    }
+    // lazy: a row whose gradient is all zero is skipped entirely (optim.py:92-95)
+    const uint64_t mask = __ballot(any);
+    const uint64_t row_bits = LPR == 64 ? mask : (mask >> ((lane / LPR) * LPR)) & ((1ull << (LPR & 63)) - 1);
+    if (a.lazy && row_bits == 0ull) return;
+    if (a.rowwise) {
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) gsq += __shfl_xor(gsq, off, 64);
+    }
+    const int64_t e0 = row * D + c0;
+    float p[4], m[4], v[4];
+    load4(t.param, a.param_bf16, e0, p);
+    load4(t.exp_avg, a.param_bf16, e0, m);
+    float v_row = 0.f, denom_row = 0.f;
+    if (a.rowwise) {
+        const float v0 = reinterpret_cast<const float *>(t.exp_avg_sq)[row];
+        v_row = fmaf(gsq / static_cast<float>(D), a.one_minus_beta2, v0 * a.beta2);
+        denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
+    } else {
+        load4(t.exp_avg_sq, a.sq_bf16, e0, v);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (a.has_decay) p[e] = p[e] * a.decay;
+        m[e] = fmaf(g[e], a.one_minus_beta1, m[e] * a.beta1);
+        float denom = denom_row;
+        if (!a.rowwise) {
+            v[e] = v[e] * a.beta2 + a.one_minus_beta2 * g[e] * g[e];
+            denom = sqrtf(v[e]) / t.sqrt_bc2 + a.eps;
+        }
+        p[e] = p[e] + (t.neg_lr_bc1 * m[e]) / denom;
+    }
+    uint32_t nz[4] = {0u, 0u, 0u, 0u};
+    if (!a.rowwise) {
+        if (a.sr && a.sq_bf16) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 2, nz);
+        store4(t.exp_avg_sq, a.sq_bf16, e0, v, a.sr, nz);
+    }
+    const bool rnd = a.sr && a.param_bf16;
+    if (rnd) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 0, nz);
+    store4(t.param, a.param_bf16, e0, p, a.sr, nz);
+    if (rnd) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 1, nz);
+    store4(t.exp_avg, a.param_bf16, e0, m, a.sr, nz);
+    if (a.rowwise && sub == 0) reinterpret_cast<float *>(t.exp_avg_sq)[row] = v_row;
+}
+
 // Standalone stochastic rounding of n fp32 values; element i uses the noise of (row i / 4096,
 // column i % 4096) of stream `stream_id` at step `step`, array 0.
 __global__ __launch_bounds__(kThreads) void sr_convert(const float *x, int64_t n, uint16_t *out,
@@ -411,8 +614,8 @@ int sort_bits(int64_t key_bound) {
 }
 
 struct DedupLayout {
-    int nblocks;
-    size_t keys_b, pos_a, pos_b, hist, heads, seg_start, total;
+    int nblocks, hist_stride;
+    size_t keys_b, pos_a, pos_b, hist, heads, seg_start, seg_pos, total;
 };
 
 DedupLayout dedup_layout(int64_t n) {
@@ -423,9 +626,11 @@ DedupLayout dedup_layout(int64_t n) {
     l.keys_b = off; off += up(static_cast<size_t>(n) * 8 * 2);  // two key buffers
     l.pos_a = off; off += up(static_cast<size_t>(n) * 4);
     l.pos_b = off; off += up(static_cast<size_t>(n) * 4);
-    l.hist = off; off += up(static_cast<size_t>(kBins) * l.nblocks * 4);
+    l.hist_stride = (l.nblocks + 3) & ~3;
+    l.hist = off; off += up(static_cast<size_t>(kBins) * l.hist_stride * 4);
     l.heads = off; off += up(static_cast<size_t>(l.nblocks + 1) * 4);
     l.seg_start = off; off += up(static_cast<size_t>(n + 1) * 4);
+    l.seg_pos = off; off += up(static_cast<size_t>(n) * 4);
     l.total = off;
     return l;
 }
@@ -471,6 +676,7 @@ extern "C" int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const
     uint32_t *hist = reinterpret_cast<uint32_t *>(ws + l.hist);
     uint32_t *heads = reinterpret_cast<uint32_t *>(ws + l.heads);
     uint32_t *seg_start = reinterpret_cast<uint32_t *>(ws + l.seg_start);
+    uint32_t *seg_pos = reinterpret_cast<uint32_t *>(ws + l.seg_pos);
 
     const int passes = (sort_bits(key_bound) + 7) / 8;
     const uint64_t *kin = reinterpret_cast<const uint64_t *>(keys);
@@ -479,11 +685,9 @@ extern "C" int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const
     int cur = 0;
     for (int p = 0; p < passes; ++p) {
         const int shift = 8 * p;
-        hipLaunchKernelGGL(rs_hist, grid, block, 0, s, kin, n, shift, hist, l.nblocks);
-        hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(kScanThreads), 0, s, hist,
-                           static_cast<int64_t>(kBins) * l.nblocks, nullptr);
+        hipLaunchKernelGGL(rs_hist, grid, block, 0, s, kin, n, shift, hist, l.nblocks, l.hist_stride);
         hipLaunchKernelGGL(rs_scatter, grid, block, 0, s, kin, pin, kb[cur], pb[cur], n, shift, hist,
-                           l.nblocks);
+                           l.hist_stride);
         kin = kb[cur];
         pin = pb[cur];
         cur ^= 1;
@@ -491,28 +695,35 @@ extern "C" int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const
     int st = check_launch("me_dedup (sort)");
     if (st != ME_OK) return st;
     hipLaunchKernelGGL(seg_count, grid, block, 0, s, kin, n, heads);
-    hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(kScanThreads), 0, s, heads,
-                       static_cast<int64_t>(l.nblocks), count);
-    hipLaunchKernelGGL(seg_write, grid, block, 0, s, kin, pin, n, heads, uniq, inv, seg_start);
+    hipLaunchKernelGGL(seg_write, grid, block, 0, s, kin, pin, n, heads, l.nblocks, uniq, inv,
+                       seg_start, seg_pos, count);
     st = check_launch("me_dedup (segments)");
     if (st != ME_OK || grads == nullptr) return st;
-    const bool vec = dim % 4 == 0;
+    // four columns per thread when every row start is aligned for the vector loads and stores
+    const size_t gsz = grad_dtype == ME_F32 ? 4 : 2;
+    const bool vec = dim % 4 == 0 && reinterpret_cast<uintptr_t>(grads) % (4 * gsz) == 0 &&
+                     reinterpret_cast<uintptr_t>(gsum) % 16 == 0;
     const int64_t threads = n * (vec ? dim / 4 : dim);
+    ME_CHECK_ARG(threads < (int64_t{1} << 31), "n * dim = %lld too large for one call",
+                 (long long)(n * dim));
     const dim3 sgrid(static_cast<unsigned>(ceil_div(threads, kThreads)));
+    const uint32_t d = static_cast<uint32_t>(dim), ns = static_cast<uint32_t>(n);
     if (grad_dtype == ME_F32) {
+        const float *g = static_cast<const float *>(grads);
         if (vec)
-            hipLaunchKernelGGL((seg_sum<float, 4>), sgrid, block, 0, s, static_cast<const float *>(grads),
-                               dim, pin, seg_start, count, n, gsum);
+            hipLaunchKernelGGL((seg_sum<float, 4>), sgrid, block, 0, s, g, d, pin, seg_start, seg_pos,
+                               count, ns, gsum);
         else
-            hipLaunchKernelGGL((seg_sum<float, 1>), sgrid, block, 0, s, static_cast<const float *>(grads),
-                               dim, pin, seg_start, count, n, gsum);
+            hipLaunchKernelGGL((seg_sum<float, 1>), sgrid, block, 0, s, g, d, pin, seg_start, seg_pos,
+                               count, ns, gsum);
     } else {
+        const uint16_t *g = static_cast<const uint16_t *>(grads);
         if (vec)
-            hipLaunchKernelGGL((seg_sum<uint16_t, 4>), sgrid, block, 0, s,
-                               static_cast<const uint16_t *>(grads), dim, pin, seg_start, count, n, gsum);
+            hipLaunchKernelGGL((seg_sum<uint16_t, 4>), sgrid, block, 0, s, g, d, pin, seg_start,
+                               seg_pos, count, ns, gsum);
         else
-            hipLaunchKernelGGL((seg_sum<uint16_t, 1>), sgrid, block, 0, s,
-                               static_cast<const uint16_t *>(grads), dim, pin, seg_start, count, n, gsum);
+            hipLaunchKernelGGL((seg_sum<uint16_t, 1>), sgrid, block, 0, s, g, d, pin, seg_start,
+                               seg_pos, count, ns, gsum);
     }
     return check_launch("me_dedup (sums)");
 }
@@ -596,8 +807,35 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
         a.n_tables = nk;
         a.total = total;
         if (total == 0) continue;
-        const dim3 grid(static_cast<unsigned>(ceil_div(total, kThreads / 64)));
-        hipLaunchKernelGGL(adam_rows, grid, dim3(kThreads), 0, as_stream(stream), a);
+        // vector path: dim = 4 * lanes-per-row with lanes-per-row a power of two <= 64, and every
+        // row start aligned for 4-element loads
+        const int lpr = dim % 4 == 0 ? dim / 4 : 0;
+        bool vec = lpr >= 1 && lpr <= 64 && (lpr & (lpr - 1)) == 0;
+        const uintptr_t pal = a.param_bf16 ? 8 : 16, val = a.rowwise ? 4 : (a.sq_bf16 ? 8 : 16);
+        for (int q = 0; q < nk && vec; ++q) {
+            const AdamTable &t = a.t[q];
+            vec = reinterpret_cast<uintptr_t>(t.param) % pal == 0 &&
+                  reinterpret_cast<uintptr_t>(t.exp_avg) % pal == 0 &&
+                  reinterpret_cast<uintptr_t>(t.exp_avg_sq) % val == 0 &&
+                  reinterpret_cast<uintptr_t>(t.grads) % 16 == 0;
+        }
+        hipStream_t s = as_stream(stream);
+        if (vec) {
+            const int64_t per_block = (64 / lpr) * (kThreads / 64);
+            const dim3 grid(static_cast<unsigned>(ceil_div(total, per_block)));
+            switch (lpr) {
+                case 1: hipLaunchKernelGGL(adam_rows_vec<1>, grid, dim3(kThreads), 0, s, a); break;
+                case 2: hipLaunchKernelGGL(adam_rows_vec<2>, grid, dim3(kThreads), 0, s, a); break;
+                case 4: hipLaunchKernelGGL(adam_rows_vec<4>, grid, dim3(kThreads), 0, s, a); break;
+                case 8: hipLaunchKernelGGL(adam_rows_vec<8>, grid, dim3(kThreads), 0, s, a); break;
+                case 16: hipLaunchKernelGGL(adam_rows_vec<16>, grid, dim3(kThreads), 0, s, a); break;
+                case 32: hipLaunchKernelGGL(adam_rows_vec<32>, grid, dim3(kThreads), 0, s, a); break;
+                default: hipLaunchKernelGGL(adam_rows_vec<64>, grid, dim3(kThreads), 0, s, a); break;
+            }
+        } else {
+            const dim3 grid(static_cast<unsigned>(ceil_div(total, kThreads / 64)));
+            hipLaunchKernelGGL(adam_rows, grid, dim3(kThreads), 0, s, a);
+        }
         const int st = check_launch("me_sparse_adam");
         if (st != ME_OK) return st;
     }
