@@ -230,6 +230,45 @@ int me_sparse_adam(int32_t n_tables, void *const *params, void *const *exp_avgs,
 int me_stochastic_bf16(const float *x, int64_t n, uint16_t *out, uint64_t seed, uint32_t step,
                        uint32_t stream_id, void *stream);
 
+/*
+ * me_fill_engram_ids -- the serving step's [tokens, max_order] matrix of each scheduled token
+ * and the ones before it, -1 where there is none (the input of me_hash_prev).
+ * Replaces fill_engram_ids (micro_engram_vllm/ids.py:10-59), and with media ids also
+ * mask_media (ids.py:62-70) in the same launch.
+ *
+ *   out            int32 [out_rows, out_row_stride]; rows [0, num_tokens_padded) are written,
+ *                  rows from num_tokens on are -1 (graph padding)
+ *   input_ids, positions      [>= num_tokens] this step's tokens (requests back to back)
+ *   idx_mapping    [>= num_reqs] request -> row of all_token_ids
+ *   query_start_loc [>= num_reqs + 1] first token of each request
+ *   all_token_ids  [hist_rows, hist_row_stride], hist_len valid columns: each request's tokens
+ *   media_ids      nullable, n_media <= 64 ids: entries equal to one of them become -1 and
+ *                  keep_out[t] (nullable, uint8 [num_tokens_padded]) is 0 where column 0 is one
+ *   *_dtype        ME_I32 or ME_I64
+ *
+ * Token t of request r: column 0 = input_ids[t]; column k reads input_ids[t - k] when position
+ * - k >= the chunk's first position, else the history row through the reference's lookback
+ * index. History reads outside [0, hist_len) or a request row outside [0, hist_rows) give -1.
+ */
+int me_fill_engram_ids(int32_t *out, int64_t out_rows, int64_t out_row_stride, int32_t max_order,
+                       const void *input_ids, int ids_dtype, const void *positions, int pos_dtype,
+                       const void *idx_mapping, int map_dtype, const void *query_start_loc,
+                       int qsl_dtype, const void *all_token_ids, int hist_dtype, int64_t hist_rows,
+                       int64_t hist_len, int64_t hist_row_stride, int64_t num_reqs,
+                       int64_t num_tokens, int64_t num_tokens_padded, const void *media_ids,
+                       int media_dtype, int32_t n_media, uint8_t *keep_out, void *stream);
+
+/*
+ * me_mask_media -- media placeholder ids become -1; keep_out[t] = 0 where column 0 is one.
+ * Replaces mask_media (micro_engram_vllm/ids.py:62-70).
+ *
+ *   ids      [n, width] of ids_dtype, rows row_stride elements apart
+ *   ids_out  int32 [n, width] contiguous; keep_out uint8 [n]
+ */
+int me_mask_media(const void *ids, int ids_dtype, int64_t n, int64_t width, int64_t row_stride,
+                  const void *media_ids, int media_dtype, int32_t n_media, int32_t *ids_out,
+                  uint8_t *keep_out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,7 +27,10 @@ sparse_adam_step         micro_engram/optim.py:65-133 (sparse branch)     == tor
                                                                           invariants (test_optim.py:56-65,
                                                                           84-88)
 fill_engram_ids          micro_engram_vllm/ids.py:10-59                   brute-force expected() of
-                                                                          test_vllm_ids.py:59-65
+                                                                          test_vllm_ids.py:59-65 over its
+                                                                          six step kinds (84-98)
+mask_media               micro_engram_vllm/ids.py:62-70                   the multimodal cases of
+                                                                          test_vllm_ids.py:135-160
 """
 import ctypes
 import os
@@ -306,27 +309,36 @@ def sparse_adam_step(p, m, v, rows, g, step, lr, betas=(0.9, 0.999), eps=1e-8, w
 def fill_engram_ids(out, input_ids, positions, idx_mapping, query_start_loc, all_token_ids,
                     num_reqs, num_tokens, num_tokens_padded):
     """micro_engram_vllm/ids.py:10-59 restated with explicit loops (numpy, small cases):
-    out[t] = (token at t, token at t-1, ...), -1 where there is none; tokens before this step's
-    chunk come from the request's history row."""
+    out[t] = (token at t, token at t-1, ...), -1 where there is none. Token t belongs to the
+    request whose query_start_loc range holds it; an earlier token in the same chunk (position
+    >= the chunk's first position) is read from input_ids[t - k], one before the chunk from the
+    request's history row through the reference's lookback index
+    j = clamp(chunk_start - 1 - q, 0, max_order - 2) (ids.py:42-55)."""
     out = np.asarray(out)
     max_order = out.shape[1]
     qsl = np.asarray(query_start_loc, dtype=np.int64)
-    for r in range(num_reqs):
-        b, e = int(qsl[r]), int(qsl[r + 1])
-        if b >= num_tokens:
-            continue
-        chunk_start = int(positions[b])
-        hist = all_token_ids[int(idx_mapping[r])]
-        for t in range(b, min(e, num_tokens)):
-            p = int(positions[t])
-            out[t, 0] = input_ids[t]
-            for k in range(1, max_order):
-                q = p - k
-                if q >= chunk_start:
-                    out[t, k] = input_ids[t - k]
-                elif q >= 0:
-                    out[t, k] = hist[q]
-                else:
-                    out[t, k] = -1
+    if num_tokens > 0:
+        for r in range(num_reqs):
+            b, e = int(qsl[r]), int(qsl[r + 1])
+            start = int(positions[min(b, num_tokens - 1)])
+            hist = np.asarray(all_token_ids)[int(idx_mapping[r])]
+            look = [int(hist[start - 1 - j]) if start - 1 - j >= 0 else -1 for j in range(max_order - 1)]
+            for t in range(b, min(e, num_tokens)):
+                p = int(positions[t])
+                out[t, 0] = input_ids[t]
+                for k in range(1, max_order):
+                    q = p - k
+                    if q >= start:
+                        out[t, k] = input_ids[max(t - k, 0)]
+                    else:
+                        out[t, k] = look[min(max(start - 1 - q, 0), max_order - 2)]
     out[num_tokens:num_tokens_padded] = -1
     return out
+
+
+def mask_media(ids, media_ids):
+    """micro_engram_vllm/ids.py:62-70: media placeholder ids become -1 (missing history);
+    keep[t] is False where the token itself (column 0) is a media placeholder."""
+    ids = np.asarray(ids)
+    is_media = np.isin(ids, np.asarray(media_ids))
+    return np.where(is_media, -1, ids).astype(ids.dtype), ~is_media[:, 0]
