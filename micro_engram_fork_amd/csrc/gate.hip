@@ -24,8 +24,8 @@
 // ring (5 x 32 KiB): buffer_load ... lds moves each 16-byte chunk straight from memory into
 // LDS (no VGPR staging), three slabs ahead of the MFMAs; out-of-range rows or K read as zeros
 // through the buffer's range check. Within a row the four 16-byte chunks are XOR-swizzled by
-// ((row >> 1) & 3), so a wave's ds_read_b128 of 32 rows at one k hits distinct banks in every
-// 8-lane group. Each slab is two 16-wide k-steps; the workgroup barrier sits between them, so
+// ((row >> 2) & 3), so the 16 lanes a ds_read_b128 serves per cycle (16 consecutive rows at one
+// logical chunk) cover all 64 LDS banks. Each slab is two 16-wide k-steps; the workgroup barrier sits between them, so
 // the next slab's first fragments are read while the current slab's second k-step runs.
 // Epilogues: each wave stages its 128 x 128 tile of round_T(C) in LDS, then walks token rows
 // with 16 lanes x 16 bytes per row, so every hidden load and output store is a coalesced
@@ -168,7 +168,7 @@ template <typename T>
 __device__ __forceinline__ void load_frag(const uint8_t *slot, int ks, int wj, int wn, int lane,
                                           Frag<T> &f) {
     const int r = lane & 31;
-    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 3)) << 4;
+    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 2) & 3)) << 4;
     using V = decltype(f.a[0]);
     using VV = typename std::remove_reference<V>::type;
 #pragma unroll
@@ -251,8 +251,8 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     const int32x4 rsrc_w = buffer_rsrc(a.w, a.w_bytes);
     const int32x4 rsrc_m = buffer_rsrc(a.mem, a.mem_bytes);
     // lane l of LDS segment s (16 rows) fills row 16 s + l / 4, physical chunk l % 4, which holds
-    // the logical chunk (l % 4) ^ ((row >> 1) & 3) of the row's slab
-    const uint32_t chunk = static_cast<uint32_t>((lane & 3) ^ ((lane >> 3) & 3)) * 16u;
+    // the logical chunk (l % 4) ^ ((row >> 2) & 3) of the row's slab
+    const uint32_t chunk = static_cast<uint32_t>((lane & 3) ^ ((lane >> 4) & 3)) * 16u;
     uint32_t offw[kDmaPerOperand], offm[kDmaPerOperand];
     bool okw[kDmaPerOperand], okm[kDmaPerOperand];
 #pragma unroll
