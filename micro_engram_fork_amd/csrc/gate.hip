@@ -178,6 +178,31 @@ __device__ __forceinline__ void load_frag(const uint8_t *slot, int ks, int wj, i
     }
 }
 
+// Part p of a fragment: A subtile p (p < 4) or B subtile p - 4.
+template <typename T>
+__device__ __forceinline__ void load_frag_part(const uint8_t *slot, int ks, int wj, int wn, int lane,
+                                               Frag<T> &f, int p) {
+    const int r = lane & 31;
+    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 2) & 3)) << 4;
+    using V = decltype(f.a[0]);
+    using VV = typename std::remove_reference<V>::type;
+    if (p < 4)
+        f.a[p] = *reinterpret_cast<const VV *>(slot + (wj * 128 + p * 32 + r) * kSlab + c);
+    else
+        f.b[p - 4] = *reinterpret_cast<const VV *>(slot + kOperandStage + (wn * 128 + (p - 4) * 32 + r) * kSlab + c);
+}
+
+// The product of A subtile x and B subtile y for one k-step.
+__device__ __forceinline__ void mfma_xy(const Frag<uint16_t> &f, floatx16 (&acc)[4][4], int x, int y) {
+    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x], f.b[y], acc[x][y], 0, 0, 0);
+}
+__device__ __forceinline__ void mfma_xy(const Frag<float> &f, floatx16 (&acc)[4][4], int x, int y) {
+    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].x, f.b[y].x, acc[x][y], 0, 0, 0);
+    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].y, f.b[y].y, acc[x][y], 0, 0, 0);
+    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].z, f.b[y].z, acc[x][y], 0, 0, 0);
+    acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].w, f.b[y].w, acc[x][y], 0, 0, 0);
+}
+
 __device__ __forceinline__ void mfma_step(const Frag<uint16_t> &f, floatx16 (&acc)[4][4]) {
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -264,32 +289,25 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
         offm[i] = okm[i] ? static_cast<uint32_t>(n0 + row) * row_bytes + chunk : 0u;
     }
     const uint32_t ring_lds = lds_addr(ring);
-    auto issue = [&](int kt) {
+    // load q (0 .. 2 * kDmaPerOperand - 1) of slab kt: W row segment q / 2 (q even) or mem
+    // row segment q / 2 (q odd)
+    auto issue_one = [&](int kt, int q) {
         const uint32_t kb = static_cast<uint32_t>(kt) * kSlab;
         const bool kin = kb + chunk < row_bytes;
         const uint32_t slot = ring_lds + static_cast<uint32_t>(kt % kStages) * kStageBytes;
-#pragma unroll
-        for (int i = 0; i < kDmaPerOperand; ++i) {
-            const uint32_t seg = static_cast<uint32_t>(wave * kDmaPerOperand + i) * 1024u;
+        const int i = q >> 1;
+        const uint32_t seg = static_cast<uint32_t>(wave * kDmaPerOperand + i) * 1024u;
+        if ((q & 1) == 0)
             dma16(rsrc_w, __builtin_amdgcn_readfirstlane(slot + seg),
                   okw[i] && kin ? offw[i] + kb : a.w_bytes);
+        else
             dma16(rsrc_m, __builtin_amdgcn_readfirstlane(slot + kOperandStage + seg),
                   okm[i] && kin ? offm[i] + kb : a.mem_bytes);
-        }
     };
-    // wait until at most `later` slabs issued after the awaited one are still in flight
-    auto wait_slab = [&](int later) {
-        constexpr int kLoads = 2 * kDmaPerOperand;  // vmcnt of one slab
-        if (later >= 3)
-            wait_vmcnt<3 * kLoads>();
-        else if (later == 2)
-            wait_vmcnt<2 * kLoads>();
-        else if (later == 1)
-            wait_vmcnt<kLoads>();
-        else
-            wait_vmcnt<0>();
+    auto issue = [&](int kt) {
+#pragma unroll
+        for (int q = 0; q < 2 * kDmaPerOperand; ++q) issue_one(kt, q);
     };
-
     floatx16 acc[4][4];
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -298,27 +316,61 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.f;
 
-    for (int kt = 0; kt < min(slabs, kStages - 1); ++kt) issue(kt);
-    wait_slab(min(slabs - 1, kStages - 2));
+    // Every slab iteration issues exactly one slab of DMA (2 * kDmaPerOperand loads): slabs past
+    // the end are issued with out-of-range offsets, which write zeros into the slot being
+    // recycled (never one still to be read). So the loads issued after any awaited slab are
+    // always the same number and every wait is a constant: kStages - 2 slabs in flight behind
+    // the one needed.
+    constexpr int kSlabLoads = 2 * kDmaPerOperand;
+    static_assert((kStages - 2) * kSlabLoads <= 63, "vmcnt counts up to 63");
+#pragma unroll
+    for (int kt = 0; kt < kStages - 1; ++kt) issue(kt);
+    wait_vmcnt<(kStages - 2) * kSlabLoads>();
     __syncthreads();
     Frag<T> f0, f1;
     load_frag<T>(ring, 0, wj, wn, lane, f0);
+    // Every non-MFMA instruction of a slab is issued between MFMAs, where it costs the matrix
+    // pipe nothing: k-step 0 carries the reads of k-step 1's fragments; k-step 1 issues four
+    // MFMAs, passes the barrier (slab kt+1 landed, slab kt-1's slot free), then carries the
+    // DMA of slab kt+4 and the reads of slab kt+1's first fragments (the parts its first
+    // MFMAs need come first). sched_barrier pins this order.
+    constexpr int kFragOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};  // a0, b0..b3, a1..a3
     for (int kt = 0; kt < slabs; ++kt) {
         const uint8_t *slot = ring + (kt % kStages) * kStageBytes;
-        load_frag<T>(slot, 1, wj, wn, lane, f1);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_step(f0, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt + 1 < slabs) {
-            wait_slab(min(slabs - 2 - kt, kStages - 3));
-            __syncthreads();  // slab kt+1 is in LDS; every wave is done reading slab kt-1
-            if (kt + kStages - 1 < slabs) issue(kt + kStages - 1);
-            load_frag<T>(ring + ((kt + 1) % kStages) * kStageBytes, 0, wj, wn, lane, f0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            mfma_xy(f0, acc, i >> 2, i & 3);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i & 1) {
+                load_frag_part<T>(slot, 1, wj, wn, lane, f1, kFragOrder[i >> 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            mfma_xy(f1, acc, i >> 2, i & 3);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wait_vmcnt<(kStages - 3) * kSlabLoads>();  // slab kt+1 (slabs kt+2, kt+3 may fly)
+        __syncthreads();  // slab kt+1 is in LDS; every wave is done reading slab kt-1
         __builtin_amdgcn_sched_barrier(0);
-        mfma_step(f1, acc);
-        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *next = ring + ((kt + 1) % kStages) * kStageBytes;
+#pragma unroll
+        for (int i = 4; i < 16; ++i) {
+            mfma_xy(f1, acc, i >> 2, i & 3);
+            __builtin_amdgcn_sched_barrier(0);
+            const int q = i - 4;
+            if (q < kSlabLoads) {
+                issue_one(kt + kStages - 1, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (q < 8) {  // past the last slab these read a stale slot; they are not used
+                load_frag_part<T>(next, 0, wj, wn, lane, f0, kFragOrder[q]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
     }
+    wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
     __syncthreads();  // the ring is free for the epilogue
 
     // ---- epilogue: each wave stages round_T of its 128 x 128 tile as [token][column] rows
