@@ -100,7 +100,8 @@ struct Chunk<2> {
     using T = uint16_t;
 };
 
-template <int MODE, int VEC>
+// GATHER = false: hash only (no memory vectors), its own instantiation without phase 3.
+template <int MODE, int VEC, bool GATHER>
 __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
     using V = typename Chunk<VEC>::T;
     __shared__ int64_t s_tok[64 * ME_MAX_ORDER];  // [tpb][max_order] hashed token values
@@ -188,42 +189,49 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
             r = h;
             if (a.idx_out != nullptr) a.idx_out[wk * a.n + g0 + wi] = r;
         }
-        if (a.mem != nullptr)
+        if (GATHER)
             s_src[wi * nt + wk] = valid ? base + static_cast<uint64_t>(r) * a.row_bytes : 0ull;
     }
-    if (a.mem == nullptr) return;  // uniform: hash-only launch
+    if (!GATHER) return;
     __syncthreads();
 
     // ---- phase 3: copy the block's memory vectors, chunk c of the block's output run. A
     // thread's chunks are walked in an order rotated by the block index, so that at any moment
     // the workgroups write different 4 KiB pieces of their runs instead of all writing the
     // same piece (runs are equal-sized and adjacent).
+    // Three straight passes per batch of kUnroll chunks: every source address (LDS reads, one
+    // wait), then every load, then every store, so all of a thread's loads are in flight at once.
     const int total = ntok * nt * a.cpr;
     uint8_t *dst = a.mem + static_cast<uint64_t>(g0) * nt * a.row_bytes;
     for (int c0 = tid; c0 < total; c0 += kBlock * kUnroll) {
         const int steps = min(kUnroll, (total - (c0 - tid) + kBlock - 1) / kBlock);
         const int rot = static_cast<int>(blockIdx.x % static_cast<unsigned>(steps));
-        V v[kUnroll];
+        int chunk[kUnroll];
+        uint64_t src[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int ur = u < steps ? (u + rot < steps ? u + rot : u + rot - steps) : u;
             const int c = c0 + ur * kBlock;
-            v[u] = V{};
+            chunk[u] = c;
+            src[u] = 0;
             if (c < total) {
                 const int p = a.cpr_shift >= 0 ? (c >> a.cpr_shift) : (c / a.cpr);
                 const int off = c - p * a.cpr;
-                const uint64_t src = s_src[p];
-                if (src != 0)
-                    v[u] = *reinterpret_cast<const V *>(src + static_cast<uint64_t>(off) * VEC);
+                const uint64_t row = s_src[p];
+                src[u] = row != 0 ? row + static_cast<uint64_t>(off) * VEC : 0;
             }
+        }
+        V v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            v[u] = V{};
+            if (src[u] != 0) v[u] = *as_global_addr<const V>(src[u]);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
-            const int ur = u < steps ? (u + rot < steps ? u + rot : u + rot - steps) : u;
-            const int c = c0 + ur * kBlock;
-            if (c < total)
+            if (chunk[u] < total)
                 __builtin_nontemporal_store(
-                    v[u], reinterpret_cast<V *>(dst + static_cast<uint64_t>(c) * VEC));
+                    v[u], as_global(reinterpret_cast<V *>(dst + static_cast<uint64_t>(chunk[u]) * VEC)));
         }
     }
 }
@@ -297,10 +305,14 @@ template <int MODE>
 int launch(const LookupArgs &a, int vec, hipStream_t stream, const char *what) {
     if (a.n == 0) return ME_OK;
     const dim3 grid(static_cast<unsigned>(ceil_div(a.n, a.tpb)));
+    if (a.mem == nullptr) {
+        hipLaunchKernelGGL((lookup_kernel<MODE, 16, false>), grid, dim3(kBlock), 0, stream, a);
+        return check_launch(what);
+    }
     switch (vec) {
-        case 16: hipLaunchKernelGGL((lookup_kernel<MODE, 16>), grid, dim3(kBlock), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((lookup_kernel<MODE, 4>), grid, dim3(kBlock), 0, stream, a); break;
-        default: hipLaunchKernelGGL((lookup_kernel<MODE, 2>), grid, dim3(kBlock), 0, stream, a); break;
+        case 16: hipLaunchKernelGGL((lookup_kernel<MODE, 16, true>), grid, dim3(kBlock), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((lookup_kernel<MODE, 4, true>), grid, dim3(kBlock), 0, stream, a); break;
+        default: hipLaunchKernelGGL((lookup_kernel<MODE, 2, true>), grid, dim3(kBlock), 0, stream, a); break;
     }
     return check_launch(what);
 }

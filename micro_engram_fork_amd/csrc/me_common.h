@@ -94,6 +94,31 @@ __device__ __forceinline__ uint32_t fastmod_u32(uint32_t a, uint64_t magic, uint
 }
 
 // ---------------------------------------------------------------------------------------------
+// Global-memory view of a device address. A pointer the compiler cannot trace back to a kernel
+// argument (one rebuilt from an integer, or read out of LDS) is generic, and accesses through
+// it compile to flat_load / flat_store, which count on lgkmcnt as well as vmcnt: every later
+// wait for an LDS read then also waits for them, which serialises a thread's loads. Through
+// an address-space-1 pointer they compile to global_load / global_store, counted by vmcnt alone.
+template <typename T>
+using gmem_ptr = __attribute__((address_space(1))) T *;
+
+// Clang vector types for loads and stores through such pointers (HIP's uint2 / float4 are
+// class types, which cannot be copied out of another address space).
+typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ gmem_ptr<T> as_global(T *p) {
+    return (gmem_ptr<T>)(p);
+}
+
+template <typename T>
+__device__ __forceinline__ gmem_ptr<T> as_global_addr(uint64_t addr) {
+    return (gmem_ptr<T>)(reinterpret_cast<T *>(addr));
+}
+
+// ---------------------------------------------------------------------------------------------
 // Launch helpers.
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 

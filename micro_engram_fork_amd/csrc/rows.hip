@@ -411,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
     while (k + 1 < a.n_tables && a.t[k + 1].first <= slot) ++k;
     const AdamTable &t = a.t[k];
     const int64_t i = slot - t.first;
-    const int64_t row = t.rows[i];
+    const int64_t row = *as_global(t.rows + i);
     const int D = a.dim;
     const float *g_row = t.grads + i * D;
     float coef = 1.f;  // gradient clipping (rows.py:224-231): min(max_norm / (norm + 1e-6), 1)
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
     const int64_t prow = row * D;
     float v_row = 0.f, denom_row = 0.f;
     if (a.rowwise) {
-        const float v = reinterpret_cast<const float *>(t.exp_avg_sq)[row];
+        const float v = *as_global(reinterpret_cast<const float *>(t.exp_avg_sq) + row);
         v_row = fmaf(gsq / static_cast<float>(D), a.one_minus_beta2, v * a.beta2);
         denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
     }
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
         store_elem(t.exp_avg, a.param_bf16, prow + c, m, a.sr,
                    rnd ? sr_noise(a.seed, t.step, t.stream_id, row, c, 1) : 0u);
     }
-    if (a.rowwise && lane == 0) reinterpret_cast<float *>(t.exp_avg_sq)[row] = v_row;
+    if (a.rowwise && lane == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
 }
 
 // Four consecutive columns c0..c0+3 (c0 % 4 == 0) share one Philox call: the same noise
@@ -484,13 +484,13 @@ __device__ __forceinline__ void sr_noise4(uint64_t seed, uint32_t step, uint32_t
 
 __device__ __forceinline__ void load4(const uint8_t *base, int bf16, int64_t e0, float (&x)[4]) {
     if (bf16) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(base + e0 * 2);
+        const u32x2_v v = *as_global(reinterpret_cast<const u32x2_v *>(base + e0 * 2));
         x[0] = bf16_bits_to_float(static_cast<uint16_t>(v.x));
         x[1] = bf16_bits_to_float(static_cast<uint16_t>(v.x >> 16));
         x[2] = bf16_bits_to_float(static_cast<uint16_t>(v.y));
         x[3] = bf16_bits_to_float(static_cast<uint16_t>(v.y >> 16));
     } else {
-        const float4 v = *reinterpret_cast<const float4 *>(base + e0 * 4);
+        const f32x4_v v = *as_global(reinterpret_cast<const f32x4_v *>(base + e0 * 4));
         x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
     }
 }
@@ -502,9 +502,9 @@ __device__ __forceinline__ void store4(uint8_t *base, int bf16, int64_t e0, cons
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             h[e] = sr ? stochastic_bf16_bits(x[e], nz[e]) : float_to_bf16_bits_rne(x[e]);
-        *reinterpret_cast<uint2 *>(base + e0 * 2) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        *as_global(reinterpret_cast<u32x2_v *>(base + e0 * 2)) = u32x2_v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     } else {
-        *reinterpret_cast<float4 *>(base + e0 * 4) = make_float4(x[0], x[1], x[2], x[3]);
+        *as_global(reinterpret_cast<f32x4_v *>(base + e0 * 4)) = f32x4_v{x[0], x[1], x[2], x[3]};
     }
 }
 
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     const AdamTable &t = s_t[lo];
     const int c0 = 4 * sub;
     const int64_t i = slot - t.first;
-    const int64_t row = t.rows[i];
+    const int64_t row = *as_global(t.rows + i);
     float g[4];
     load4(reinterpret_cast<const uint8_t *>(t.grads), 0, i * D + c0, g);
     float coef = 1.f;  // gradient clipping (rows.py:224-231): min(max_norm / (norm + 1e-6), 1)
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     load4(t.exp_avg, a.param_bf16, e0, m);
     float v_row = 0.f, denom_row = 0.f;
     if (a.rowwise) {
-        const float v0 = reinterpret_cast<const float *>(t.exp_avg_sq)[row];
+        const float v0 = *as_global(reinterpret_cast<const float *>(t.exp_avg_sq) + row);
         v_row = fmaf(gsq / static_cast<float>(D), a.one_minus_beta2, v0 * a.beta2);
         denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
     } else {
@@ -593,7 +593,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     store4(t.param, a.param_bf16, e0, p, a.sr, nz);
     if (rnd) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 1, nz);
     store4(t.exp_avg, a.param_bf16, e0, m, a.sr, nz);
-    if (a.rowwise && sub == 0) reinterpret_cast<float *>(t.exp_avg_sq)[row] = v_row;
+    if (a.rowwise && sub == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
 }
 
 // Standalone stochastic rounding of n fp32 values; element i uses the noise of (row i / 4096,
