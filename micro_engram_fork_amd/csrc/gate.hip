@@ -20,13 +20,18 @@
 // GEMM tiling: a 256-thread workgroup owns a 256 (model dims j) x 256 (tokens n) output tile;
 // its four waves each hold 128 x 128 as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (fp32 engrams:
 // v_mfma_f32_32x32x2f32). Both operands are K-contiguous in HBM (W is [d, M], mem is [N, M]).
-// The K loop streams 64-byte k-slabs of all 256 A rows and 256 B rows through a 5-slot LDS
-// ring (5 x 32 KiB): buffer_load ... lds moves each 16-byte chunk straight from memory into
-// LDS (no VGPR staging), three slabs ahead of the MFMAs; out-of-range rows or K read as zeros
-// through the buffer's range check. Within a row the four 16-byte chunks are XOR-swizzled by
-// ((row >> 2) & 3), so the 16 lanes a ds_read_b128 serves per cycle (16 consecutive rows at one
-// logical chunk) cover all 64 LDS banks. Each slab is two 16-wide k-steps; the workgroup barrier sits between them, so
-// the next slab's first fragments are read while the current slab's second k-step runs.
+// The K loop streams 128-byte k-slabs (one cache line of every one of the 256 A rows and 256
+// B rows) through five 32 KiB LDS units: slab s's A rows go to unit 2s % 5 and its B rows to
+// unit (2s + 1) % 5, so two slabs' worth of loads are in flight while one is consumed.
+// buffer_load ... lds moves each 16-byte chunk straight from memory into LDS (no VGPR
+// staging); one instruction fills 8 whole 128-byte rows, so every L2 request is a full line
+// (64-byte slabs asked for each line twice, and the L1 address path, not the L2, set the
+// pace). Out-of-range rows or K read as zeros through the buffer's range check. Within a row
+// the eight 16-byte chunks are XOR-swizzled by ((row >> 1) & 7), so the 16 lanes a
+// ds_read_b128 serves per cycle (16 consecutive rows at one logical chunk) cover all 64 LDS
+// banks. A slab is four 16-wide k-steps and one workgroup barrier, placed in the last k-step:
+// every fragment read of the slab is done by then, so the loads refilling its units and the
+// reads of the next slab's first fragments run under that k-step's MFMAs.
 // Epilogues: each wave stages its 128 x 128 tile of round_T(C) in LDS, then walks token rows
 // with 16 lanes x 16 bytes per row, so every hidden load and output store is a coalesced
 // 256-byte row segment. The key pass reduces its three sums per row across the 16 lanes with
@@ -48,12 +53,11 @@ typedef int int32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kTile = 256;                         // output tile edge (j and n)
-constexpr int kSlab = 64;                          // bytes of K per row per ring slot
-constexpr int kStages = 5;                         // ring slots (3 slabs in flight)
-constexpr int kOperandStage = kTile * kSlab;       // 16 KiB
-constexpr int kStageBytes = 2 * kOperandStage;     // A (W rows) + B (mem rows)
-constexpr int kRingBytes = kStages * kStageBytes;  // 160 KiB
-constexpr int kDmaPerOperand = kOperandStage / (kThreads * 16);  // 16-byte loads per thread
+constexpr int kSlab = 128;                         // bytes of K per row per slab (a cache line)
+constexpr int kUnit = kTile * kSlab;               // 32 KiB: one operand of one slab
+constexpr int kUnits = 5;
+constexpr int kRingBytes = kUnits * kUnit;         // 160 KiB
+constexpr int kDmaPerOperand = kUnit / (kThreads * 16);  // 16-byte loads per thread: 8
 constexpr int kStagePitch = 256 + 8;               // epilogue staging row: 256 B + pad
 constexpr int kWaveStage = 128 * kStagePitch;      // one wave's staged 128-row tile
 constexpr int kGroupTiles = 8;                     // token tiles per XCD group
@@ -148,11 +152,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // ---- MFMA k-steps ----------------------------------------------------------------------------
-// A slot holds swizzled [256 rows][64 B] tiles of A and B; a slab is two 16-wide (bf16) k-steps.
-// The wave's A rows are wj*128 + [0,128), its B rows wn*128 + [0,128). For k-step ks, lane l
-// reads row (l & 31) of each 32-row subtile at logical chunk 2*ks + (l >> 5): lanes 0-31 carry
-// one half of the step's k values and lanes 32-63 the other, identically for A and B, which is
-// all the dot product needs.
+// A slab's A rows sit in LDS unit ua and its B rows in unit ub, [256 rows][128 B] swizzled; a
+// slab is four 16-wide (bf16) k-steps. The wave's A rows are wj*128 + [0,128), its B rows
+// wn*128 + [0,128). For k-step ks, lane l reads row (l & 31) of each 32-row subtile at logical
+// chunk 2*ks + (l >> 5): lanes 0-31 carry one half of the step's k values and lanes 32-63 the
+// other, identically for A and B, which is all the dot product needs.
 template <typename T>
 struct Frag;
 template <>
@@ -164,32 +168,18 @@ struct Frag<float> {
     float4 a[4], b[4];
 };
 
-template <typename T>
-__device__ __forceinline__ void load_frag(const uint8_t *slot, int ks, int wj, int wn, int lane,
-                                          Frag<T> &f) {
-    const int r = lane & 31;
-    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 2) & 3)) << 4;
-    using V = decltype(f.a[0]);
-    using VV = typename std::remove_reference<V>::type;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        f.a[s] = *reinterpret_cast<const VV *>(slot + (wj * 128 + s * 32 + r) * kSlab + c);
-        f.b[s] = *reinterpret_cast<const VV *>(slot + kOperandStage + (wn * 128 + s * 32 + r) * kSlab + c);
-    }
-}
-
 // Part p of a fragment: A subtile p (p < 4) or B subtile p - 4.
 template <typename T>
-__device__ __forceinline__ void load_frag_part(const uint8_t *slot, int ks, int wj, int wn, int lane,
-                                               Frag<T> &f, int p) {
+__device__ __forceinline__ void load_frag_part(const uint8_t *ua, const uint8_t *ub, int ks, int wj,
+                                               int wn, int lane, Frag<T> &f, int p) {
     const int r = lane & 31;
-    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 2) & 3)) << 4;
+    const int c = ((2 * ks + (lane >> 5)) ^ ((r >> 1) & 7)) << 4;
     using V = decltype(f.a[0]);
     using VV = typename std::remove_reference<V>::type;
     if (p < 4)
-        f.a[p] = *reinterpret_cast<const VV *>(slot + (wj * 128 + p * 32 + r) * kSlab + c);
+        f.a[p] = *reinterpret_cast<const VV *>(ua + (wj * 128 + p * 32 + r) * kSlab + c);
     else
-        f.b[p - 4] = *reinterpret_cast<const VV *>(slot + kOperandStage + (wn * 128 + (p - 4) * 32 + r) * kSlab + c);
+        f.b[p - 4] = *reinterpret_cast<const VV *>(ub + (wn * 128 + (p - 4) * 32 + r) * kSlab + c);
 }
 
 // The product of A subtile x and B subtile y for one k-step.
@@ -201,26 +191,6 @@ __device__ __forceinline__ void mfma_xy(const Frag<float> &f, floatx16 (&acc)[4]
     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].y, f.b[y].y, acc[x][y], 0, 0, 0);
     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].z, f.b[y].z, acc[x][y], 0, 0, 0);
     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].w, f.b[y].w, acc[x][y], 0, 0, 0);
-}
-
-__device__ __forceinline__ void mfma_step(const Frag<uint16_t> &f, floatx16 (&acc)[4][4]) {
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y)
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x], f.b[y], acc[x][y], 0, 0, 0);
-}
-
-__device__ __forceinline__ void mfma_step(const Frag<float> &f, floatx16 (&acc)[4][4]) {
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y) {
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].x, f.b[y].x, acc[x][y], 0, 0, 0);
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].y, f.b[y].y, acc[x][y], 0, 0, 0);
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].z, f.b[y].z, acc[x][y], 0, 0, 0);
-            acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].w, f.b[y].w, acc[x][y], 0, 0, 0);
-        }
 }
 
 // Sum over the 16 lanes of a DPP row (lanes 16i .. 16i+15), exact in lane 16i + 15: an inclusive
@@ -270,44 +240,38 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     float alpha_reg = 0.f;
     if (PHASE == kValue && n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
 
-    // ---- K loop over a 5-slot ring of 64-byte slabs
+    // ---- K loop over 128-byte slabs: A_s (W rows) in unit 2s % 5, B_s (mem rows) in (2s+1) % 5
     const uint32_t row_bytes = static_cast<uint32_t>(a.m * sizeof(T));
     const int slabs = static_cast<int>(ceil_div(row_bytes, kSlab));
     const int32x4 rsrc_w = buffer_rsrc(a.w, a.w_bytes);
     const int32x4 rsrc_m = buffer_rsrc(a.mem, a.mem_bytes);
-    // lane l of LDS segment s (16 rows) fills row 16 s + l / 4, physical chunk l % 4, which holds
-    // the logical chunk (l % 4) ^ ((row >> 2) & 3) of the row's slab
-    const uint32_t chunk = static_cast<uint32_t>((lane & 3) ^ ((lane >> 4) & 3)) * 16u;
-    uint32_t offw[kDmaPerOperand], offm[kDmaPerOperand];
+    // load i of a wave fills rows 8 (8 wave + i) + [0, 8): lane l writes row + l / 8 at physical
+    // chunk l % 8, which holds the row's logical chunk (l % 8) ^ ((row >> 1) & 7)
+    uint32_t offw[kDmaPerOperand], offm[kDmaPerOperand], chunk[kDmaPerOperand];
     bool okw[kDmaPerOperand], okm[kDmaPerOperand];
 #pragma unroll
     for (int i = 0; i < kDmaPerOperand; ++i) {
-        const int row = (wave * kDmaPerOperand + i) * 16 + (lane >> 2);
+        const int row = (wave * kDmaPerOperand + i) * 8 + (lane >> 3);
+        chunk[i] = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
         okw[i] = j0 + row < a.d;
         okm[i] = n0 + row < a.n;
-        offw[i] = okw[i] ? static_cast<uint32_t>(j0 + row) * row_bytes + chunk : 0u;
-        offm[i] = okm[i] ? static_cast<uint32_t>(n0 + row) * row_bytes + chunk : 0u;
+        offw[i] = okw[i] ? static_cast<uint32_t>(j0 + row) * row_bytes + chunk[i] : 0u;
+        offm[i] = okm[i] ? static_cast<uint32_t>(n0 + row) * row_bytes + chunk[i] : 0u;
     }
     const uint32_t ring_lds = lds_addr(ring);
-    // load q (0 .. 2 * kDmaPerOperand - 1) of slab kt: W row segment q / 2 (q even) or mem
-    // row segment q / 2 (q odd)
-    auto issue_one = [&](int kt, int q) {
-        const uint32_t kb = static_cast<uint32_t>(kt) * kSlab;
-        const bool kin = kb + chunk < row_bytes;
-        const uint32_t slot = ring_lds + static_cast<uint32_t>(kt % kStages) * kStageBytes;
-        const int i = q >> 1;
-        const uint32_t seg = static_cast<uint32_t>(wave * kDmaPerOperand + i) * 1024u;
-        if ((q & 1) == 0)
-            dma16(rsrc_w, __builtin_amdgcn_readfirstlane(slot + seg),
-                  okw[i] && kin ? offw[i] + kb : a.w_bytes);
+    // load i of operand op (0: A, 1: B) of slab sl
+    auto issue = [&](int sl, int op, int i) {
+        const uint32_t kb = static_cast<uint32_t>(sl) * kSlab;
+        const bool kin = kb + chunk[i] < row_bytes;
+        const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl + op) % kUnits) * kUnit +
+                             static_cast<uint32_t>(wave * kDmaPerOperand + i) * 1024u;
+        if (op == 0)
+            dma16(rsrc_w, __builtin_amdgcn_readfirstlane(dst), okw[i] && kin ? offw[i] + kb : a.w_bytes);
         else
-            dma16(rsrc_m, __builtin_amdgcn_readfirstlane(slot + kOperandStage + seg),
-                  okm[i] && kin ? offm[i] + kb : a.mem_bytes);
+            dma16(rsrc_m, __builtin_amdgcn_readfirstlane(dst), okm[i] && kin ? offm[i] + kb : a.mem_bytes);
     };
-    auto issue = [&](int kt) {
-#pragma unroll
-        for (int q = 0; q < 2 * kDmaPerOperand; ++q) issue_one(kt, q);
-    };
+    auto unit_a = [&](int sl) { return ring + ((2 * sl) % kUnits) * kUnit; };
+    auto unit_b = [&](int sl) { return ring + ((2 * sl + 1) % kUnits) * kUnit; };
     floatx16 acc[4][4];
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -316,33 +280,58 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.f;
 
-    // Every slab iteration issues exactly one slab of DMA (2 * kDmaPerOperand loads): slabs past
-    // the end are issued with out-of-range offsets, which write zeros into the slot being
-    // recycled (never one still to be read). So the loads issued after any awaited slab are
-    // always the same number and every wait is a constant: kStages - 2 slabs in flight behind
-    // the one needed.
-    constexpr int kSlabLoads = 2 * kDmaPerOperand;
-    static_assert((kStages - 2) * kSlabLoads <= 63, "vmcnt counts up to 63");
+    // Slab s issues A_{s+2} under its k-step 0 (into B_{s-1}'s unit, free since the previous
+    // barrier) and B_{s+2} after its barrier (into A_s's unit). Slabs past the end are issued
+    // with out-of-range offsets, which write zeros into units nobody reads, so the number of
+    // loads issued after any awaited one is fixed and every wait is a constant.
 #pragma unroll
-    for (int kt = 0; kt < kStages - 1; ++kt) issue(kt);
-    wait_vmcnt<(kStages - 2) * kSlabLoads>();
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < kDmaPerOperand; ++i) issue(sl, op, i);
+    wait_vmcnt<2 * kDmaPerOperand>();  // A_0, B_0 landed (A_1, B_1 may fly)
     __syncthreads();
     Frag<T> f0, f1;
-    load_frag<T>(ring, 0, wj, wn, lane, f0);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) load_frag_part<T>(unit_a(0), unit_b(0), 0, wj, wn, lane, f0, p);
     // Every non-MFMA instruction of a slab is issued between MFMAs, where it costs the matrix
-    // pipe nothing: k-step 0 carries the reads of k-step 1's fragments; k-step 1 issues four
-    // MFMAs, passes the barrier (slab kt+1 landed, slab kt-1's slot free), then carries the
-    // DMA of slab kt+4 and the reads of slab kt+1's first fragments (the parts its first
-    // MFMAs need come first). sched_barrier pins this order.
+    // pipe nothing: k-steps 0-2 carry the reads of the next k-step's fragments (k-step 0 also
+    // the loads of A_{s+2}); k-step 3 issues four MFMAs, waits for slab s+1 (A_{s+2} may still
+    // fly), passes the barrier (every wave is done reading slab s), then carries the loads of
+    // B_{s+2} and the reads of slab s+1's first fragments (the parts its first MFMAs need
+    // come first). sched_barrier pins this order.
     constexpr int kFragOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};  // a0, b0..b3, a1..a3
-    for (int kt = 0; kt < slabs; ++kt) {
-        const uint8_t *slot = ring + (kt % kStages) * kStageBytes;
+    for (int sl = 0; sl < slabs; ++sl) {
+        const uint8_t *ua = unit_a(sl), *ub = unit_b(sl);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            mfma_xy(f0, acc, i >> 2, i & 3);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i < kDmaPerOperand) {
+                issue(sl + 2, 0, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (i & 1) {
+                load_frag_part<T>(ua, ub, 1, wj, wn, lane, f1, kFragOrder[i >> 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            mfma_xy(f1, acc, i >> 2, i & 3);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i & 1) {
+                load_frag_part<T>(ua, ub, 2, wj, wn, lane, f0, kFragOrder[i >> 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             mfma_xy(f0, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
             if (i & 1) {
-                load_frag_part<T>(slot, 1, wj, wn, lane, f1, kFragOrder[i >> 1]);
+                load_frag_part<T>(ua, ub, 3, wj, wn, lane, f1, kFragOrder[i >> 1]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -351,21 +340,21 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             mfma_xy(f1, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
         }
-        wait_vmcnt<(kStages - 3) * kSlabLoads>();  // slab kt+1 (slabs kt+2, kt+3 may fly)
-        __syncthreads();  // slab kt+1 is in LDS; every wave is done reading slab kt-1
+        wait_vmcnt<kDmaPerOperand>();  // slab s+1 landed (A_{s+2} may still fly)
+        __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        const uint8_t *next = ring + ((kt + 1) % kStages) * kStageBytes;
+        const uint8_t *na = unit_a(sl + 1), *nb = unit_b(sl + 1);
 #pragma unroll
         for (int i = 4; i < 16; ++i) {
             mfma_xy(f1, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
             const int q = i - 4;
-            if (q < kSlabLoads) {
-                issue_one(kt + kStages - 1, q);
+            if (q < kDmaPerOperand) {
+                issue(sl + 2, 1, q);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (q < 8) {  // past the last slab these read a stale slot; they are not used
-                load_frag_part<T>(next, 0, wj, wn, lane, f0, kFragOrder[q]);
+            if (q < 8) {  // past the last slab these read a stale unit; they are not used
+                load_frag_part<T>(na, nb, 0, wj, wn, lane, f0, kFragOrder[q]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
