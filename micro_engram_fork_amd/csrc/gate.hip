@@ -80,6 +80,7 @@ struct GateArgs {
     float *alpha_eff;       // [n] gate of each token, 0 where keep is false
     int64_t n, d, m;
     uint32_t mem_bytes, w_bytes;  // buffer ranges (reads past them return zeros)
+    uint32_t hidden_bytes, scale_bytes;  // ranges of the prefetched epilogue operands
     int scale_bf16;
     int sqrt_mode;
     int n_jt, n_nt, total_tiles, per_xcd;
@@ -193,6 +194,16 @@ __device__ __forceinline__ void mfma_xy(const Frag<float> &f, floatx16 (&acc)[4]
     acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[x].w, f.b[y].w, acc[x][y], 0, 0, 0);
 }
 
+// Element e of an accumulator tile, read out of its accumulation register in program order.
+// The staging after the K loop reads one subtile at a time this way: left to itself the
+// compiler copies all 256 accumulators into VGPRs at the loop exit, which leaves no room for
+// anything else live there (the prefetched epilogue operands).
+__device__ __forceinline__ float acc_read(const floatx16 &t, int e) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(t[e]));
+    return v;
+}
+
 // Sum over the 16 lanes of a DPP row (lanes 16i .. 16i+15), exact in lane 16i + 15: an inclusive
 // scan by row shifts of 1, 2, 4 and 8 (out-of-row sources read as 0).
 __device__ __forceinline__ float row16_sum(float v) {
@@ -215,7 +226,10 @@ __device__ __forceinline__ float gate_alpha(float sx2, float sk2, float sck, con
     return 1.0f / (1.0f + expf(-s));
 }
 
-template <typename T, typename H, int PHASE>
+// PF: the epilogue's hidden rows (and the key pass's scales) are loaded into registers under
+// the last k-slabs, so their latency and the HBM burst of every CU reaching its epilogue at
+// once overlap the MFMAs (bf16 tiles and hidden under 2 GiB: 32 rows x 16 bytes per lane).
+template <typename T, typename H, int PHASE, bool PF>
 __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kRingBytes];
 
@@ -239,6 +253,47 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     // the value pass reads its tokens' gates now; they are parked in LDS after the K loop
     float alpha_reg = 0.f;
     if (PHASE == kValue && n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
+
+    // ---- epilogue row walk geometry (the prefetch below uses it): 16 lanes x 16 bytes per token
+    // row, lane l16 owning kLaneCols columns, rows rsub, rsub + 4, ... of the wave's 128
+    constexpr int kPasses = sizeof(T) == 2 ? 1 : 2;
+    constexpr int kPassCols = 128 / kPasses;     // columns staged per pass
+    constexpr int kLaneCols = 16 / sizeof(T);    // columns per lane in the row walk (8 / 4)
+    constexpr int kRowWords = kLaneCols * sizeof(H) / 4;  // hidden words per lane per row
+    constexpr int kBatch = kRowWords <= 4 ? 32 : 16;      // rows whose hidden loads are in flight
+    static_assert(!PF || (kPasses == 1 && kRowWords == 4 && kBatch == 32), "prefetch geometry");
+    const int l16 = lane & 15, rsub = lane >> 4;
+    const int64_t ntok0 = n0 + wn * 128;          // first token of the wave
+    // prefetched epilogue operands: 32 hidden rows, and (key pass) 2 x 2 words of the scale
+    // deltas (bf16 deltas use the first of each pair); every load is issued for every lane
+    // (out-of-range offsets read zeros), so their number is fixed
+    constexpr int kPfLoads = 32 + (PHASE == kKey ? 4 : 0);
+    u32x4_v xpre[PF ? 32 : 1];
+    u32x4_v spre[PF && PHASE == kKey ? 4 : 1];
+    auto prefetch = [&]() {
+        const int64_t jl = j0 + wj * 128 + l16 * kLaneCols;
+        const bool jok = jl < a.d;
+        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            const int64_t n = ntok0 + u * 4 + rsub;
+            const uint32_t off = jok && n < a.n ? static_cast<uint32_t>((n * a.d + jl) * 2) : a.hidden_bytes;
+            xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0));
+        }
+        if constexpr (PHASE == kKey) {
+            const int esz = a.scale_bf16 ? 2 : 4;
+            const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
+            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+            spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+            spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
+            spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+            spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+        }
+    };
 
     // ---- K loop over 128-byte slabs: A_s (W rows) in unit 2s % 5, B_s (mem rows) in (2s+1) % 5
     const uint32_t row_bytes = static_cast<uint32_t>(a.m * sizeof(T));
@@ -302,13 +357,19 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     // B_{s+2} and the reads of slab s+1's first fragments (the parts its first MFMAs need
     // come first). sched_barrier pins this order.
     constexpr int kFragOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};  // a0, b0..b3, a1..a3
-    for (int sl = 0; sl < slabs; ++sl) {
+    // The slab loop is peeled around the prefetch, which goes out at the end of slab pf_at,
+    // right behind the last real slab's loads (B_{slabs-1}). The slabs after it issue no
+    // loads (all theirs would be past the end), so the prefetched registers share the tail
+    // only with the fragments, and the slab after it waits for its slab behind the prefetch.
+    const int pf_at = PF ? max(slabs - 3, 0) : slabs;
+    static_assert(kPfLoads <= 63, "vmcnt counts up to 63");
+    auto slab = [&](int sl, auto wait, auto dma) {
         const uint8_t *ua = unit_a(sl), *ub = unit_b(sl);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             mfma_xy(f0, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
-            if (i < kDmaPerOperand) {
+            if (decltype(dma)::value && i < kDmaPerOperand) {
                 issue(sl + 2, 0, i);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -340,7 +401,10 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             mfma_xy(f1, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
         }
-        wait_vmcnt<kDmaPerOperand>();  // slab s+1 landed (A_{s+2} may still fly)
+        // slab s+1 landed: A_{s+2} (or, in the slab after the prefetch, the prefetch) may still
+        // fly; past the last slab there is nothing to wait for
+        if constexpr (decltype(wait)::value == 1) wait_vmcnt<kDmaPerOperand>();
+        if constexpr (decltype(wait)::value == 2) wait_vmcnt<kPfLoads>();
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t *na = unit_a(sl + 1), *nb = unit_b(sl + 1);
@@ -349,7 +413,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             mfma_xy(f1, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
             const int q = i - 4;
-            if (q < kDmaPerOperand) {
+            if (decltype(dma)::value && q < kDmaPerOperand) {
                 issue(sl + 2, 1, q);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -358,6 +422,18 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+    };
+    using WaitSlab = std::integral_constant<int, 1>;
+    using WaitPrefetch = std::integral_constant<int, 2>;
+    using NoWait = std::integral_constant<int, 0>;
+    using Dma = std::true_type;
+    using NoDma = std::false_type;
+    for (int sl = 0; sl < pf_at; ++sl) slab(sl, WaitSlab{}, Dma{});
+    if constexpr (PF) {
+        slab(pf_at, WaitSlab{}, Dma{});
+        prefetch();
+        if (pf_at + 1 < slabs) slab(pf_at + 1, WaitPrefetch{}, NoDma{});
+        for (int sl = pf_at + 2; sl < slabs; ++sl) slab(sl, NoWait{}, NoDma{});
     }
     wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
     __syncthreads();  // the ring is free for the epilogue
@@ -365,16 +441,9 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     // ---- epilogue: each wave stages round_T of its 128 x 128 tile as [token][column] rows
     // (pitch kStagePitch), then walks its token rows with 16 lanes x 16 bytes per row. fp32
     // tiles go in two column halves of 64.
-    constexpr int kPasses = sizeof(T) == 2 ? 1 : 2;
-    constexpr int kPassCols = 128 / kPasses;     // columns staged per pass
-    constexpr int kLaneCols = 16 / sizeof(T);    // columns per lane in the row walk (8 / 4)
-    constexpr int kRowWords = kLaneCols * sizeof(H) / 4;  // hidden words per lane per row
-    constexpr int kBatch = kRowWords <= 4 ? 32 : 16;      // rows whose hidden loads are in flight
     uint8_t *stage = ring + wave * kWaveStage;
     float *s_aux = reinterpret_cast<float *>(ring + 4 * kWaveStage);  // [2][256][3] or [256]
     const int r = lane & 31, half = lane >> 5;
-    const int l16 = lane & 15, rsub = lane >> 4;  // row walk: lane column block, row in 4
-    const int64_t ntok0 = n0 + wn * 128;          // first token of the wave
 
     if (PHASE == kValue) {
         s_aux[tid] = alpha_reg;
@@ -395,10 +464,11 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
                     uint32_t w[sizeof(T)];
                     T *tv = reinterpret_cast<T *>(w);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) tv[e] = from_f<T>(acc[x][y][4 * g + e]);
+                    for (int e = 0; e < 4; ++e) tv[e] = from_f<T>(acc_read(acc[x][y], 4 * g + e));
                     uint8_t *p = stage + (y * 32 + r) * kStagePitch + col * sizeof(T);
                     reinterpret_cast<uint2 *>(p)[0] = make_uint2(w[0], w[1]);
                     if (sizeof(T) == 4) reinterpret_cast<uint2 *>(p)[1] = make_uint2(w[2], w[3]);
+                    if (g == 3) __builtin_amdgcn_sched_barrier(0);
                 }
         }
         __syncthreads();  // staging (and s_aux) visible
@@ -408,7 +478,22 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
         float wcol[kLaneCols];  // q_scale * k_scale of the lane's columns (key pass)
 #pragma unroll
         for (int e = 0; e < kLaneCols; ++e) wcol[e] = 1.f;
-        if (PHASE == kKey && jok && a.q_delta != nullptr) {
+        if (PF && PHASE == kKey && jok && a.q_delta != nullptr) {
+            const uint32_t *qw = reinterpret_cast<const uint32_t *>(&spre[0]);
+            const uint32_t *kw = reinterpret_cast<const uint32_t *>(&spre[2]);
+#pragma unroll
+            for (int e = 0; e < kLaneCols; ++e) {
+                float qv, kv;
+                if (a.scale_bf16) {
+                    qv = bf16_bits_to_float(static_cast<uint16_t>(qw[e / 2] >> (16 * (e & 1))));
+                    kv = bf16_bits_to_float(static_cast<uint16_t>(kw[e / 2] >> (16 * (e & 1))));
+                } else {
+                    qv = __uint_as_float(qw[e]);
+                    kv = __uint_as_float(kw[e]);
+                }
+                wcol[e] = (1.f + qv) * (1.f + kv);
+            }
+        } else if (PHASE == kKey && jok && a.q_delta != nullptr) {
             float qv[kLaneCols], kv[kLaneCols];
             if (a.scale_bf16) {
                 load_run<uint16_t, kLaneCols>(static_cast<const uint8_t *>(a.q_delta) + jl * 2, qv);
@@ -426,7 +511,10 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             for (int u = 0; u < kBatch; ++u) {
                 const int row = (b0 + u) * 4 + rsub;
                 const int64_t n = ntok0 + row;
-                if (jok && n < a.n) {
+                if constexpr (PF) {
+#pragma unroll
+                    for (int q = 0; q < kRowWords; ++q) xr[u][q] = xpre[u][q];
+                } else if (jok && n < a.n) {
                     const uint8_t *p = a.hidden + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
 #pragma unroll
                     for (int q = 0; q < kRowWords; q += 2) {
@@ -593,6 +681,14 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     a.m = mem_dim;
     a.mem_bytes = static_cast<uint32_t>(n * mem_dim * esz);
     a.w_bytes = static_cast<uint32_t>(model_dim * mem_dim * esz);
+    const int64_t hidden_bytes = n * model_dim * static_cast<int64_t>(dtype_size(hidden_dtype));
+    // the prefetching kernels address hidden with 32-bit buffer offsets
+    const bool prefetch = dtype == ME_BF16 && hidden_dtype == ME_BF16 &&
+                          hidden_bytes < (int64_t{1} << 31);
+    a.hidden_bytes = prefetch ? static_cast<uint32_t>(hidden_bytes) : 0u;
+    a.scale_bytes = gate_mode == ME_GATE_SCALAR_SQRT
+                        ? static_cast<uint32_t>(model_dim * (scale_dtype == ME_BF16 ? 2 : 4))
+                        : 0u;
     a.n_jt = static_cast<int>(ceil_div(model_dim, kTile));
     a.n_nt = static_cast<int>(ceil_div(n, kTile));
     a.total_tiles = a.n_jt * a.n_nt;
@@ -606,23 +702,26 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     ak.w = static_cast<const uint8_t *>(w_key);
     av.w = static_cast<const uint8_t *>(w_value);
     const dim3 grid(static_cast<unsigned>(a.per_xcd * kXcds));
-#define ME_GATE_LAUNCH(T, H)                                                                     \
+#define ME_GATE_LAUNCH(T, H, PF)                                                                 \
     do {                                                                                         \
-        hipLaunchKernelGGL((gate_kernel<T, H, kKey>), grid, dim3(kThreads), 0, s, ak);          \
+        hipLaunchKernelGGL((gate_kernel<T, H, kKey, PF>), grid, dim3(kThreads), 0, s, ak);      \
         int st_ = check_launch("me_gate_residual (key pass)");                                  \
         if (st_ != ME_OK) return st_;                                                            \
         hipLaunchKernelGGL(gate_alpha_kernel, dim3(static_cast<unsigned>(ceil_div(n, kThreads))), \
                            dim3(kThreads), 0, s, ak);                                            \
         st_ = check_launch("me_gate_residual (gate)");                                           \
         if (st_ != ME_OK) return st_;                                                            \
-        hipLaunchKernelGGL((gate_kernel<T, H, kValue>), grid, dim3(kThreads), 0, s, av);        \
+        hipLaunchKernelGGL((gate_kernel<T, H, kValue, PF>), grid, dim3(kThreads), 0, s, av);    \
         return check_launch("me_gate_residual (value pass)");                                   \
     } while (0)
     if (dtype == ME_BF16) {
-        if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(uint16_t, uint16_t);
-        ME_GATE_LAUNCH(uint16_t, float);
+        if (hidden_dtype == ME_BF16) {
+            if (prefetch) ME_GATE_LAUNCH(uint16_t, uint16_t, true);
+            ME_GATE_LAUNCH(uint16_t, uint16_t, false);
+        }
+        ME_GATE_LAUNCH(uint16_t, float, false);
     }
-    if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(float, uint16_t);
-    ME_GATE_LAUNCH(float, float);
+    if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(float, uint16_t, false);
+    ME_GATE_LAUNCH(float, float, false);
 #undef ME_GATE_LAUNCH
 }

@@ -156,9 +156,11 @@ def test_golden_inject_fixture():
     assert_close_out(out, torch.from_numpy(f["out"]), t["hidden"], torch.float32)
 
 
-@pytest.mark.parametrize("n,d,dim,heads", [(300, 264, 8, 3), (513, 1024, 16, 2), (7, 4096, 64, 8)])
+@pytest.mark.parametrize("n,d,dim,heads", [(300, 264, 8, 3), (513, 1024, 16, 2), (7, 4096, 64, 8),
+                                            (600, 776, 64, 8), (1100, 520, 32, 5)])
 def test_ragged_shapes_bf16(n, d, dim, heads):
-    # token counts and model dims that are not multiples of the 256 tile
+    # token counts and model dims that are not multiples of the 256 tile; K from 2 to 24
+    # 128-byte slabs (the epilogue operands are prefetched under the last slabs)
     torch.manual_seed(n)
     eng = _make(torch.bfloat16, d=d, dim=dim, heads=heads, orders=(2, 3, 4))
     ids = torch.randint(0, 1000, (1, n), device=DEV)
