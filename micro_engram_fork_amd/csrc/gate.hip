@@ -271,27 +271,29 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     u32x4_v xpre[PF ? 32 : 1];
     u32x4_v spre[PF && PHASE == kKey ? 4 : 1];
     auto prefetch = [&]() {
-        const int64_t jl = j0 + wj * 128 + l16 * kLaneCols;
-        const bool jok = jl < a.d;
-        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+        if constexpr (PF) {
+            const int64_t jl = j0 + wj * 128 + l16 * kLaneCols;
+            const bool jok = jl < a.d;
+            const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
 #pragma unroll
-        for (int u = 0; u < 32; ++u) {
-            const int64_t n = ntok0 + u * 4 + rsub;
-            const uint32_t off = jok && n < a.n ? static_cast<uint32_t>((n * a.d + jl) * 2) : a.hidden_bytes;
-            xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0));
-        }
-        if constexpr (PHASE == kKey) {
-            const int esz = a.scale_bf16 ? 2 : 4;
-            const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
-            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
-            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
-            spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
-            spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
-            spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-            spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+            for (int u = 0; u < 32; ++u) {
+                const int64_t n = ntok0 + u * 4 + rsub;
+                const uint32_t off = jok && n < a.n ? static_cast<uint32_t>((n * a.d + jl) * 2) : a.hidden_bytes;
+                xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0));
+            }
+            if constexpr (PHASE == kKey) {
+                const int esz = a.scale_bf16 ? 2 : 4;
+                const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
+                const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+                const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+                spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+                spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
+                spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+                spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+            }
         }
     };
 
