@@ -155,13 +155,49 @@ int me_gate_workspace_size(int64_t n, int64_t model_dim, size_t *bytes);
  *                 ignored for ME_GATE_SCALAR
  *   keep          nullable [n] uint8 (bool): 0 leaves the token's hidden state unchanged
  *   alpha_out     nullable [n] fp32: the gate value of each token (before keep)
+ *   row_stats     nullable [n, 4] fp32: per token sum hidden^2, sum K^2, sum hidden * (1 +
+ *                 q_scale_delta) * (1 + k_scale_delta) * K (scales 1 for ME_GATE_SCALAR) and the
+ *                 gate: what me_gate_backward needs of the forward
  *   workspace     at least me_gate_workspace_size(n, model_dim) bytes
  */
 int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
                      const void *mem, int64_t mem_dim, const void *w_key, const void *w_value,
                      int dtype, const void *q_scale_delta, const void *k_scale_delta,
                      int scale_dtype, int gate_mode, const uint8_t *keep, void *out,
-                     float *alpha_out, void *workspace, size_t workspace_size, void *stream);
+                     float *alpha_out, float *row_stats, void *workspace, size_t workspace_size,
+                     void *stream);
+
+/*
+ * me_gate_backward_workspace_size -- bytes of workspace me_gate_backward needs.
+ */
+int me_gate_backward_workspace_size(int64_t n, int64_t model_dim, size_t *bytes);
+
+/*
+ * me_gate_backward -- gradients of me_gate_residual: what autograd computes through
+ * MicroEngram.inject (micro_engram/module.py:239-261) for the scalar gates, given the gradient
+ * of its output. The projections K and V are recomputed (same MFMA tiles as the forward), so
+ * the forward keeps only row_stats.
+ *
+ *   same shapes, dtypes and rules as me_gate_residual for hidden .. keep
+ *   grad_out      [n, model_dim] of hidden_dtype: gradient of out
+ *   row_stats     [n, 4] fp32 from the forward (me_gate_residual's row_stats)
+ *   grad_hidden   [n, model_dim] of hidden_dtype: grad_out + the gradient through the gate's
+ *                 rms norm of hidden, rounded to hidden_dtype first (hidden.float()'s backward)
+ *   grad_key      [n, model_dim] of dtype: gradient of K = W_K mem (the key Linear's output)
+ *   grad_value    [n, model_dim] of dtype: gradient of V = W_V mem; the weight and mem
+ *                 gradients are then plain GEMMs: dW_K = grad_key^T mem, dW_V = grad_value^T mem,
+ *                 dmem = grad_key W_K + grad_value W_V
+ *   grad_q/k_scale  [model_dim] fp32: gradients of q_scale_delta / k_scale_delta (needed for
+ *                 ME_GATE_SCALAR_SQRT, ignored otherwise)
+ *   workspace     at least me_gate_backward_workspace_size(n, model_dim) bytes
+ */
+int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                     const void *mem, int64_t mem_dim, const void *w_key, const void *w_value,
+                     int dtype, const void *q_scale_delta, const void *k_scale_delta,
+                     int scale_dtype, int gate_mode, const uint8_t *keep, const void *grad_out,
+                     const float *row_stats, void *grad_hidden, void *grad_key, void *grad_value,
+                     float *grad_q_scale, float *grad_k_scale, void *workspace,
+                     size_t workspace_size, void *stream);
 
 /*
  * me_dedup_workspace_size -- bytes of workspace me_dedup needs for n keys.

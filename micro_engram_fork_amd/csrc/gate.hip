@@ -65,7 +65,8 @@ constexpr int kXcds = 8;
 constexpr uint32_t kBufferConfig = 0x00020000u;    // raw buffer descriptor word 3 (gfx9 family)
 static_assert(4 * kWaveStage + 2 * kTile * 3 * 4 <= kRingBytes, "epilogue must fit in the ring");
 
-enum Phase : int { kKey = 0, kValue = 1 };
+// Forward passes (key, value) and the backward's two passes over the same GEMM tiles.
+enum Phase : int { kKey = 0, kValue = 1, kGradValue = 2, kGradKey = 3 };
 
 struct GateArgs {
     const uint8_t *hidden;  // [n, d] of H
@@ -81,6 +82,15 @@ struct GateArgs {
     int64_t n, d, m;
     uint32_t mem_bytes, w_bytes;  // buffer ranges (reads past them return zeros)
     uint32_t hidden_bytes, scale_bytes;  // ranges of the prefetched epilogue operands
+    float *row_stats_out;   // forward, nullable: [n][4] sum x^2, sum K^2, sum x qs ks K, alpha
+    // backward
+    const uint8_t *grad_out;   // [n, d] of H: gradient of the output
+    const float *row_stats;    // [n][4] the forward's row_stats_out
+    uint8_t *grad_hidden;      // [n, d] of H
+    uint8_t *grad_proj;        // [n, d] of T: dV (value side) or dK (key side)
+    float *grad_partials;      // [n_jt][n] per-column-tile sums of g . V
+    float *tok_coef;           // [n][3] per-token coefficients of the key side (a, c2, c3)
+    float *col_partials;       // [n_nt][d] per-token-tile column sums of a x K
     int scale_bf16;
     int sqrt_mode;
     int n_jt, n_nt, total_tiles, per_xcd;
@@ -253,6 +263,17 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     // the value pass reads its tokens' gates now; they are parked in LDS after the K loop
     float alpha_reg = 0.f;
     if (PHASE == kValue && n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
+    // the backward's value side: the gate of the token with keep folded in; key side: the
+    // token's coefficients (zero past the last token, so those rows add nothing)
+    float coef_reg[3] = {0.f, 0.f, 0.f};
+    if (PHASE == kGradValue && n0 + tid < a.n) {
+        alpha_reg = a.row_stats[(n0 + tid) * 4 + 3];
+        if (a.keep != nullptr && a.keep[n0 + tid] == 0) alpha_reg = 0.f;
+    }
+    if (PHASE == kGradKey && n0 + tid < a.n) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) coef_reg[c] = a.tok_coef[(n0 + tid) * 3 + c];
+    }
 
     // ---- epilogue row walk geometry (the prefetch below uses it): 16 lanes x 16 bytes per token
     // row, lane l16 owning kLaneCols columns, rows rsub, rsub + 4, ... of the wave's 128
@@ -447,10 +468,21 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     float *s_aux = reinterpret_cast<float *>(ring + 4 * kWaveStage);  // [2][256][3] or [256]
     const int r = lane & 31, half = lane >> 5;
 
+    // s_aux: key [2 wj][256 tokens][3] sums; value [256] gates; grad value [256] gates then
+    // [2 wj][256] sums of g . V; grad key [256][3] coefficients then [2 wn][256 columns]
     if (PHASE == kValue) {
         s_aux[tid] = alpha_reg;
-    } else {
+    } else if (PHASE == kKey) {
         for (int e = tid; e < 2 * kTile * 3; e += kThreads) s_aux[e] = 0.f;
+    } else if (PHASE == kGradValue) {
+        s_aux[tid] = alpha_reg;
+        s_aux[kTile + tid] = 0.f;
+        s_aux[2 * kTile + tid] = 0.f;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) s_aux[tid * 3 + c] = coef_reg[c];
+        s_aux[3 * kTile + tid] = 0.f;
+        s_aux[4 * kTile + tid] = 0.f;
     }
 
     for (int pass = 0; pass < kPasses; ++pass) {
@@ -469,7 +501,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
                     for (int e = 0; e < 4; ++e) tv[e] = from_f<T>(acc_read(acc[x][y], 4 * g + e));
                     uint8_t *p = stage + (y * 32 + r) * kStagePitch + col * sizeof(T);
                     reinterpret_cast<uint2 *>(p)[0] = make_uint2(w[0], w[1]);
-                    if (sizeof(T) == 4) reinterpret_cast<uint2 *>(p)[1] = make_uint2(w[2], w[3]);
+                    if constexpr (sizeof(T) == 4) reinterpret_cast<uint2 *>(p)[1] = make_uint2(w[2], w[3]);
                     if (g == 3) __builtin_amdgcn_sched_barrier(0);
                 }
         }
@@ -480,6 +512,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
         float wcol[kLaneCols];  // q_scale * k_scale of the lane's columns (key pass)
 #pragma unroll
         for (int e = 0; e < kLaneCols; ++e) wcol[e] = 1.f;
+        constexpr bool kScaled = PHASE == kKey || PHASE == kGradKey;
         if (PF && PHASE == kKey && jok && a.q_delta != nullptr) {
             const uint32_t *qw = reinterpret_cast<const uint32_t *>(&spre[0]);
             const uint32_t *kw = reinterpret_cast<const uint32_t *>(&spre[2]);
@@ -495,7 +528,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
                 }
                 wcol[e] = (1.f + qv) * (1.f + kv);
             }
-        } else if (PHASE == kKey && jok && a.q_delta != nullptr) {
+        } else if (kScaled && jok && a.q_delta != nullptr) {
             float qv[kLaneCols], kv[kLaneCols];
             if (a.scale_bf16) {
                 load_run<uint16_t, kLaneCols>(static_cast<const uint8_t *>(a.q_delta) + jl * 2, qv);
@@ -507,30 +540,50 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 #pragma unroll
             for (int e = 0; e < kLaneCols; ++e) wcol[e] = (1.f + qv[e]) * (1.f + kv[e]);
         }
-        for (int b0 = 0; b0 < 32; b0 += kBatch) {
-            uint32_t xr[kBatch][kRowWords];
+        // rows of hidden (forward, key side of the backward) or of the output gradient (value
+        // side); the key side of the backward reads both, in half-size batches
+        constexpr int kRowBatch = PHASE == kGradKey ? kBatch / 2 : kBatch;
+        float colp[kLaneCols];  // grad key: sums of a x K over the lane's rows
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
+        for (int e = 0; e < kLaneCols; ++e) colp[e] = 0.f;
+        const uint8_t *src0 = PHASE == kGradValue ? a.grad_out : a.hidden;
+        for (int b0 = 0; b0 < 32; b0 += kRowBatch) {
+            uint32_t xr[kRowBatch][kRowWords];
+            uint32_t gr[PHASE == kGradKey ? kRowBatch : 1][kRowWords];
+#pragma unroll
+            for (int u = 0; u < kRowBatch; ++u) {
                 const int row = (b0 + u) * 4 + rsub;
                 const int64_t n = ntok0 + row;
                 if constexpr (PF) {
 #pragma unroll
                     for (int q = 0; q < kRowWords; ++q) xr[u][q] = xpre[u][q];
                 } else if (jok && n < a.n) {
-                    const uint8_t *p = a.hidden + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
+                    const int64_t off = (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
 #pragma unroll
                     for (int q = 0; q < kRowWords; q += 2) {
-                        const uint2 v = reinterpret_cast<const uint2 *>(p)[q / 2];
+                        const uint2 v = reinterpret_cast<const uint2 *>(src0 + off)[q / 2];
                         xr[u][q] = v.x;
                         xr[u][q + 1] = v.y;
+                    }
+                    if constexpr (PHASE == kGradKey) {
+#pragma unroll
+                        for (int q = 0; q < kRowWords; q += 2) {
+                            const uint2 v = reinterpret_cast<const uint2 *>(a.grad_out + off)[q / 2];
+                            gr[u][q] = v.x;
+                            gr[u][q + 1] = v.y;
+                        }
                     }
                 } else {
 #pragma unroll
                     for (int q = 0; q < kRowWords; ++q) xr[u][q] = 0u;
+                    if constexpr (PHASE == kGradKey) {
+#pragma unroll
+                        for (int q = 0; q < kRowWords; ++q) gr[u][q] = 0u;
+                    }
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
+            for (int u = 0; u < kRowBatch; ++u) {
                 const int row = (b0 + u) * 4 + rsub;
                 const int64_t n = ntok0 + row;
                 const uint8_t *sp = stage + row * kStagePitch + (l16 * kLaneCols) * sizeof(T);
@@ -559,21 +612,83 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
                         p[1] += sck;
                         p[2] += sx2;
                     }
-                } else if (jok && n < a.n) {
+                } else if (PHASE == kValue) {
+                    if (jok && n < a.n) {
+                        const float alpha = s_aux[wn * 128 + row];
+                        uint32_t ow[kRowWords];
+                        H *ov = reinterpret_cast<H *>(ow);
+#pragma unroll
+                        for (int e = 0; e < kLaneCols; ++e)
+                            ov[e] = from_f<H>(to_f<H>(xv[e]) + round_t<H>(alpha * to_f<T>(cv[e])));
+                        // non-temporal: the output is not read again by this kernel, and written
+                        // through it leaves no dirty lines for the next kernel's traffic to evict
+                        uint8_t *p = a.out + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
+#pragma unroll
+                        for (int q = 0; q < kRowWords; q += 2)
+                            __builtin_nontemporal_store(u32x2_t{ow[q], ow[q + 1]},
+                                                        reinterpret_cast<u32x2_t *>(p) + q / 2);
+                    }
+                } else if (PHASE == kGradValue) {
+                    // d alpha gets sum_j g_j V_j (keep is applied per token later); dV = alpha g,
+                    // rounded to the engram dtype as the cast after the projection rounds it
                     const float alpha = s_aux[wn * 128 + row];
-                    uint32_t ow[kRowWords];
-                    H *ov = reinterpret_cast<H *>(ow);
+                    float gv = 0.f;
+                    uint32_t dw[4];
+                    T *dv = reinterpret_cast<T *>(dw);
 #pragma unroll
-                    for (int e = 0; e < kLaneCols; ++e)
-                        ov[e] = from_f<H>(to_f<H>(xv[e]) + round_t<H>(alpha * to_f<T>(cv[e])));
-                    // non-temporal: the output is not read again by this kernel, and written
-                    // through it leaves no dirty lines for the next kernel's traffic to evict
-                    uint8_t *p = a.out + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
+                    for (int e = 0; e < kLaneCols; ++e) {
+                        const float g = to_f<H>(xv[e]);
+                        gv += g * to_f<T>(cv[e]);
+                        dv[e] = from_f<T>(alpha * g);
+                    }
+                    gv = row16_sum(gv);
+                    if (l16 == 15) s_aux[kTile + wj * kTile + wn * 128 + row] += gv;
+                    if (jok && n < a.n) {
+                        uint8_t *p = a.grad_proj + (n * a.d + jl) * static_cast<int64_t>(sizeof(T));
+                        *reinterpret_cast<uint4 *>(p) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+                    }
+                } else {  // kGradKey
+                    // with the token's coefficients (ca, c2, c3) and w = q_scale k_scale:
+                    //   d hidden = g + round(ca w K - c2 x), dK = ca w x - c3 K, scales: ca x K
+                    const float *cf = s_aux + (wn * 128 + row) * 3;
+                    const float ca = cf[0], c2 = cf[1], c3 = cf[2];
+                    const H *gv = reinterpret_cast<const H *>(gr[u]);
+                    uint32_t hw[kRowWords], kw[4];
+                    H *hv = reinterpret_cast<H *>(hw);
+                    T *kv = reinterpret_cast<T *>(kw);
 #pragma unroll
-                    for (int q = 0; q < kRowWords; q += 2)
-                        __builtin_nontemporal_store(u32x2_t{ow[q], ow[q + 1]},
-                                                    reinterpret_cast<u32x2_t *>(p) + q / 2);
+                    for (int e = 0; e < kLaneCols; ++e) {
+                        const float K = to_f<T>(cv[e]);
+                        const float x = to_f<H>(xv[e]);
+                        const float dx = ca * wcol[e] * K - c2 * x;
+                        hv[e] = from_f<H>(to_f<H>(gv[e]) + round_t<H>(dx));
+                        kv[e] = from_f<T>(ca * wcol[e] * x - c3 * K);
+                        colp[e] += ca * x * K;
+                    }
+                    if (jok && n < a.n) {
+                        const int64_t off = n * a.d + jl;
+                        uint8_t *ph = a.grad_hidden + off * static_cast<int64_t>(sizeof(H));
+#pragma unroll
+                        for (int q = 0; q < kRowWords; q += 2)
+                            reinterpret_cast<uint2 *>(ph)[q / 2] = make_uint2(hw[q], hw[q + 1]);
+                        uint8_t *pk = a.grad_proj + off * static_cast<int64_t>(sizeof(T));
+                        *reinterpret_cast<uint4 *>(pk) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+                    }
                 }
+            }
+        }
+        if constexpr (PHASE == kGradKey) {
+            // column sums over the wave's 128 tokens: the four row groups of a column block are
+            // lanes l16, l16 + 16, l16 + 32, l16 + 48
+#pragma unroll
+            for (int e = 0; e < kLaneCols; ++e) {
+                colp[e] += __shfl_xor(colp[e], 16, 64);
+                colp[e] += __shfl_xor(colp[e], 32, 64);
+            }
+            if (rsub == 0) {
+                const int c0 = wj * 128 + pass * kPassCols + l16 * kLaneCols;
+#pragma unroll
+                for (int e = 0; e < kLaneCols; ++e) s_aux[(3 + wn) * kTile + c0 + e] = colp[e];
             }
         }
         __syncthreads();  // the staging area is reused by the next pass; s_aux is complete
@@ -589,6 +704,16 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             o[1] = p0[1] + p1[1];
             o[2] = p0[2] + p1[2];
         }
+    } else if (PHASE == kGradValue) {
+        const int64_t n = n0 + tid;
+        if (n < a.n)
+            a.grad_partials[static_cast<int64_t>(jt) * a.n + n] =
+                s_aux[kTile + tid] + s_aux[2 * kTile + tid];
+    } else if (PHASE == kGradKey) {
+        const int64_t j = j0 + tid;
+        if (j < a.d)
+            a.col_partials[static_cast<int64_t>(nt) * a.d + j] =
+                s_aux[3 * kTile + tid] + s_aux[4 * kTile + tid];
     }
 }
 
@@ -607,8 +732,68 @@ __global__ __launch_bounds__(kThreads) void gate_alpha_kernel(const GateArgs a) 
     }
     float alpha = gate_alpha(sx2, sk2, sck, a);
     if (a.alpha_out != nullptr) a.alpha_out[n] = alpha;
+    if (a.row_stats_out != nullptr) {
+        float *st = a.row_stats_out + n * 4;
+        st[0] = sx2;
+        st[1] = sk2;
+        st[2] = sck;
+        st[3] = alpha;
+    }
     if (a.keep != nullptr && a.keep[n] == 0) alpha = 0.f;
     a.alpha_eff[n] = alpha;
+}
+
+// Backward, per token, between its value side and its key side (module.py:240-251 under
+// autograd). With r_h = rsqrt(mean x^2 + eps), r_k = rsqrt(mean K^2 + eps), s0 = r_h r_k sck /
+// sqrt(d) (sck = sum x qs ks K) and alpha = sigmoid(s):
+//   d alpha = keep * sum_j g_j V_j;  ds = d alpha * alpha (1 - alpha)
+//   scalar_sqrt: s = sign(s0) sqrt(max(|s0|, 1e-6)) -> ds0 = ds / (2 sqrt|s0|) where |s0| >= 1e-6
+//   (clamp_min passes the gradient at and above the bound), else 0; scalar gate: ds0 = ds
+// and the rms-norm backward of h = x r_h qs and k = K r_k ks reduces to three coefficients
+//   a = ds0 r_h r_k / sqrt(d), c2 = a r_h^2 sck / d, c3 = a r_k^2 sck / d
+// with dx_j = a qs_j ks_j K_j - c2 x_j and dK_j = a qs_j ks_j x_j - c3 K_j (the sums the rms
+// norm's backward needs, sum du u and sum dv v, are both r_h r_k ds0 sck / sqrt(d)).
+__global__ __launch_bounds__(kThreads) void gate_grad_token_kernel(const GateArgs a) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (n >= a.n) return;
+    constexpr float kEps = 1.1920928955078125e-07f;
+    const float *st = a.row_stats + n * 4;
+    const float sx2 = st[0], sk2 = st[1], sck = st[2], alpha = st[3];
+    float dalpha = 0.f;
+#pragma unroll 8
+    for (int t = 0; t < a.n_jt; ++t) dalpha += a.grad_partials[static_cast<int64_t>(t) * a.n + n];
+    if (a.keep != nullptr && a.keep[n] == 0) dalpha = 0.f;
+    const float ds = dalpha * alpha * (1.f - alpha);
+    const float rh = 1.0f / sqrtf(sx2 * a.inv_d + kEps);
+    const float rk = 1.0f / sqrtf(sk2 * a.inv_d + kEps);
+    const float s0 = rh * rk * sck * a.inv_sqrt_d;
+    float ds0 = ds;
+    if (a.sqrt_mode) ds0 = fabsf(s0) >= 1e-6f ? ds / (2.f * sqrtf(fabsf(s0))) : 0.f;
+    const float ca = ds0 * rh * rk * a.inv_sqrt_d;
+    float *cf = a.tok_coef + n * 3;
+    cf[0] = ca;
+    cf[1] = ca * rh * rh * sck * a.inv_d;
+    cf[2] = ca * rk * rk * sck * a.inv_d;
+}
+
+// Backward of the scale deltas: P_j = sum over tokens of a x_j K_j (per token tile, then here),
+// d q_scale_j = k_scale_j P_j and d k_scale_j = q_scale_j P_j (scale = 1 + delta).
+__global__ __launch_bounds__(kThreads) void gate_grad_scale_kernel(const GateArgs a, float *grad_q,
+                                                                   float *grad_k) {
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (j >= a.d) return;
+    float pj = 0.f;
+    for (int t = 0; t < a.n_nt; ++t) pj += a.col_partials[static_cast<int64_t>(t) * a.d + j];
+    float q, k;
+    if (a.scale_bf16) {
+        q = bf16_bits_to_float(static_cast<const uint16_t *>(a.q_delta)[j]);
+        k = bf16_bits_to_float(static_cast<const uint16_t *>(a.k_delta)[j]);
+    } else {
+        q = static_cast<const float *>(a.q_delta)[j];
+        k = static_cast<const float *>(a.k_delta)[j];
+    }
+    grad_q[j] = (1.f + k) * pj;
+    grad_k[j] = (1.f + q) * pj;
 }
 
 size_t workspace_bytes(int64_t n, int64_t d) {
@@ -616,6 +801,78 @@ size_t workspace_bytes(int64_t n, int64_t d) {
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Backward workspace: [n_jt][n] value-side partials, [n][3] token coefficients, [n_nt][d]
+// column partials (floats, each region 256-byte aligned).
+struct GradLayout {
+    size_t partials, coef, cols, total;
+};
+
+GradLayout grad_layout(int64_t n, int64_t d) {
+    auto up = [](size_t x) { return (x + 255) & ~size_t{255}; };
+    GradLayout l{};
+    size_t off = 0;
+    l.partials = off;
+    off += up(static_cast<size_t>(ceil_div(d, kTile)) * static_cast<size_t>(n) * 4);
+    l.coef = off;
+    off += up(static_cast<size_t>(n) * 3 * 4);
+    l.cols = off;
+    off += up(static_cast<size_t>(ceil_div(n, kTile)) * static_cast<size_t>(d) * 4);
+    l.total = off;
+    return l;
+}
+
+// Shape, dtype and alignment checks shared by the forward and the backward; fills the
+// arguments common to both.
+int gate_common(GateArgs &a, const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                const void *mem, int64_t mem_dim, const void *w_key, const void *w_value, int dtype,
+                const void *q_scale_delta, const void *k_scale_delta, int scale_dtype, int gate_mode,
+                const uint8_t *keep) {
+    ME_CHECK_ARG(hidden_dtype == ME_BF16 || hidden_dtype == ME_F32, "hidden dtype must be bf16/fp32");
+    ME_CHECK_ARG(dtype == ME_BF16 || dtype == ME_F32, "engram dtype must be bf16/fp32");
+    ME_CHECK_ARG(gate_mode == ME_GATE_SCALAR || gate_mode == ME_GATE_SCALAR_SQRT,
+                 "gate_mode must be ME_GATE_SCALAR or ME_GATE_SCALAR_SQRT");
+    ME_CHECK_ARG(n >= 0 && model_dim >= 1 && mem_dim >= 1, "bad shape");
+    ME_CHECK_ARG(n < (int64_t{1} << 31) && model_dim < (int64_t{1} << 24) && mem_dim < (int64_t{1} << 24),
+                 "shape too large");
+    ME_CHECK_ARG(hidden && mem && w_key && w_value, "null tensor pointer");
+    const size_t esz = dtype_size(dtype);
+    ME_CHECK_ARG((mem_dim * esz) % 16 == 0, "mem_dim * element size must be a multiple of 16 bytes");
+    ME_CHECK_ARG(model_dim % 8 == 0, "model_dim must be a multiple of 8");
+    ME_CHECK_ARG(n * mem_dim * static_cast<int64_t>(esz) < (int64_t{1} << 31) &&
+                     model_dim * mem_dim * static_cast<int64_t>(esz) < (int64_t{1} << 31),
+                 "mem and the projection weights must each be under 2 GiB");
+    ME_CHECK_ARG(aligned16(hidden) && aligned16(mem) && aligned16(w_key) && aligned16(w_value),
+                 "tensors must be 16-byte aligned");
+    if (gate_mode == ME_GATE_SCALAR_SQRT) {
+        ME_CHECK_ARG(q_scale_delta && k_scale_delta, "scalar_sqrt needs q/k scale deltas");
+        ME_CHECK_ARG(scale_dtype == ME_BF16 || scale_dtype == ME_F32, "scale dtype must be bf16/fp32");
+        ME_CHECK_ARG(aligned16(q_scale_delta) && aligned16(k_scale_delta),
+                     "scale tensors must be 16-byte aligned");
+    }
+    a.hidden = static_cast<const uint8_t *>(hidden);
+    a.mem = static_cast<const uint8_t *>(mem);
+    a.q_delta = gate_mode == ME_GATE_SCALAR_SQRT ? q_scale_delta : nullptr;
+    a.k_delta = gate_mode == ME_GATE_SCALAR_SQRT ? k_scale_delta : nullptr;
+    a.scale_bf16 = scale_dtype == ME_BF16;
+    a.sqrt_mode = gate_mode == ME_GATE_SCALAR_SQRT;
+    a.keep = keep;
+    a.n = n;
+    a.d = model_dim;
+    a.m = mem_dim;
+    a.mem_bytes = static_cast<uint32_t>(n * mem_dim * esz);
+    a.w_bytes = static_cast<uint32_t>(model_dim * mem_dim * esz);
+    a.scale_bytes = gate_mode == ME_GATE_SCALAR_SQRT
+                        ? static_cast<uint32_t>(model_dim * (scale_dtype == ME_BF16 ? 2 : 4))
+                        : 0u;
+    a.n_jt = static_cast<int>(ceil_div(model_dim, kTile));
+    a.n_nt = static_cast<int>(ceil_div(n, kTile));
+    a.total_tiles = a.n_jt * a.n_nt;
+    a.per_xcd = static_cast<int>(ceil_div(a.total_tiles, kXcds));
+    a.inv_d = 1.0f / static_cast<float>(model_dim);
+    a.inv_sqrt_d = static_cast<float>(1.0 / std::sqrt(static_cast<double>(model_dim)));
+    return ME_OK;
+}
 
 }  // namespace
 }  // namespace me
@@ -634,69 +891,30 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
                                 const void *mem, int64_t mem_dim, const void *w_key,
                                 const void *w_value, int dtype, const void *q_scale_delta,
                                 const void *k_scale_delta, int scale_dtype, int gate_mode,
-                                const uint8_t *keep, void *out, float *alpha_out, void *workspace,
-                                size_t workspace_size, void *stream) {
-    ME_CHECK_ARG(hidden_dtype == ME_BF16 || hidden_dtype == ME_F32, "hidden dtype must be bf16/fp32");
-    ME_CHECK_ARG(dtype == ME_BF16 || dtype == ME_F32, "engram dtype must be bf16/fp32");
-    ME_CHECK_ARG(gate_mode == ME_GATE_SCALAR || gate_mode == ME_GATE_SCALAR_SQRT,
-                 "gate_mode must be ME_GATE_SCALAR or ME_GATE_SCALAR_SQRT");
-    ME_CHECK_ARG(n >= 0 && model_dim >= 1 && mem_dim >= 1, "bad shape");
-    ME_CHECK_ARG(n < (int64_t{1} << 31) && model_dim < (int64_t{1} << 24) && mem_dim < (int64_t{1} << 24),
-                 "shape too large");
+                                const uint8_t *keep, void *out, float *alpha_out,
+                                float *row_stats, void *workspace, size_t workspace_size,
+                                void *stream) {
+    GateArgs a{};
     if (n == 0) return ME_OK;
-    ME_CHECK_ARG(hidden && mem && w_key && w_value && out, "null tensor pointer");
-    const size_t esz = dtype_size(dtype);
-    ME_CHECK_ARG((mem_dim * esz) % 16 == 0, "mem_dim * element size must be a multiple of 16 bytes");
-    ME_CHECK_ARG(model_dim % 8 == 0, "model_dim must be a multiple of 8");
-    ME_CHECK_ARG(n * mem_dim * static_cast<int64_t>(esz) < (int64_t{1} << 31) &&
-                     model_dim * mem_dim * static_cast<int64_t>(esz) < (int64_t{1} << 31),
-                 "mem and the projection weights must each be under 2 GiB");
-    ME_CHECK_ARG(aligned16(hidden) && aligned16(mem) && aligned16(w_key) && aligned16(w_value) &&
-                     aligned16(out),
-                 "tensors must be 16-byte aligned");
-    if (gate_mode == ME_GATE_SCALAR_SQRT) {
-        ME_CHECK_ARG(q_scale_delta && k_scale_delta, "scalar_sqrt needs q/k scale deltas");
-        ME_CHECK_ARG(scale_dtype == ME_BF16 || scale_dtype == ME_F32, "scale dtype must be bf16/fp32");
-        ME_CHECK_ARG(aligned16(q_scale_delta) && aligned16(k_scale_delta),
-                     "scale tensors must be 16-byte aligned");
-    }
+    const int st = gate_common(a, hidden, hidden_dtype, n, model_dim, mem, mem_dim, w_key, w_value,
+                               dtype, q_scale_delta, k_scale_delta, scale_dtype, gate_mode, keep);
+    if (st != ME_OK) return st;
+    ME_CHECK_ARG(out != nullptr && aligned16(out), "out must be a 16-byte aligned tensor");
     const size_t need = workspace_bytes(n, model_dim);
     if (workspace == nullptr || workspace_size < need) {
         set_error("me_gate_residual: workspace of %zu bytes needed, got %zu", need, workspace_size);
         return ME_ERR_WORKSPACE;
     }
-
-    GateArgs a{};
-    a.hidden = static_cast<const uint8_t *>(hidden);
-    a.mem = static_cast<const uint8_t *>(mem);
-    a.q_delta = gate_mode == ME_GATE_SCALAR_SQRT ? q_scale_delta : nullptr;
-    a.k_delta = gate_mode == ME_GATE_SCALAR_SQRT ? k_scale_delta : nullptr;
-    a.scale_bf16 = scale_dtype == ME_BF16;
-    a.sqrt_mode = gate_mode == ME_GATE_SCALAR_SQRT;
-    a.keep = keep;
     a.out = static_cast<uint8_t *>(out);
     a.alpha_out = alpha_out;
+    a.row_stats_out = row_stats;
     a.partials = static_cast<float *>(workspace);
     a.alpha_eff = a.partials + ceil_div(model_dim, kTile) * 3 * n;
-    a.n = n;
-    a.d = model_dim;
-    a.m = mem_dim;
-    a.mem_bytes = static_cast<uint32_t>(n * mem_dim * esz);
-    a.w_bytes = static_cast<uint32_t>(model_dim * mem_dim * esz);
     const int64_t hidden_bytes = n * model_dim * static_cast<int64_t>(dtype_size(hidden_dtype));
     // the prefetching kernels address hidden with 32-bit buffer offsets
     const bool prefetch = dtype == ME_BF16 && hidden_dtype == ME_BF16 &&
                           hidden_bytes < (int64_t{1} << 31);
     a.hidden_bytes = prefetch ? static_cast<uint32_t>(hidden_bytes) : 0u;
-    a.scale_bytes = gate_mode == ME_GATE_SCALAR_SQRT
-                        ? static_cast<uint32_t>(model_dim * (scale_dtype == ME_BF16 ? 2 : 4))
-                        : 0u;
-    a.n_jt = static_cast<int>(ceil_div(model_dim, kTile));
-    a.n_nt = static_cast<int>(ceil_div(n, kTile));
-    a.total_tiles = a.n_jt * a.n_nt;
-    a.per_xcd = static_cast<int>(ceil_div(a.total_tiles, kXcds));
-    a.inv_d = 1.0f / static_cast<float>(model_dim);
-    a.inv_sqrt_d = static_cast<float>(1.0 / std::sqrt(static_cast<double>(model_dim)));
 
     hipStream_t s = as_stream(stream);
     // the key pass reads W_K, the value pass W_V; both launches share the args
@@ -726,4 +944,95 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(float, uint16_t, false);
     ME_GATE_LAUNCH(float, float, false);
 #undef ME_GATE_LAUNCH
+}
+
+extern "C" int me_gate_backward_workspace_size(int64_t n, int64_t model_dim, size_t *bytes) {
+    ME_CHECK_ARG(bytes != nullptr, "bytes is null");
+    ME_CHECK_ARG(n >= 0 && model_dim >= 1, "bad shape n=%lld d=%lld", (long long)n,
+                 (long long)model_dim);
+    *bytes = grad_layout(n, model_dim).total;
+    return ME_OK;
+}
+
+extern "C" int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                                const void *mem, int64_t mem_dim, const void *w_key,
+                                const void *w_value, int dtype, const void *q_scale_delta,
+                                const void *k_scale_delta, int scale_dtype, int gate_mode,
+                                const uint8_t *keep, const void *grad_out, const float *row_stats,
+                                void *grad_hidden, void *grad_key, void *grad_value,
+                                float *grad_q_scale, float *grad_k_scale, void *workspace,
+                                size_t workspace_size, void *stream) {
+    GateArgs a{};
+    if (n == 0) {
+        // no tokens: the scale gradients are zero
+        if (gate_mode == ME_GATE_SCALAR_SQRT && grad_q_scale != nullptr && grad_k_scale != nullptr) {
+            hipStream_t s0 = as_stream(stream);
+            if (hipMemsetAsync(grad_q_scale, 0, model_dim * 4, s0) != hipSuccess ||
+                hipMemsetAsync(grad_k_scale, 0, model_dim * 4, s0) != hipSuccess)
+                return check_launch("me_gate_backward (zero scale gradients)");
+        }
+        return ME_OK;
+    }
+    const int st = gate_common(a, hidden, hidden_dtype, n, model_dim, mem, mem_dim, w_key, w_value,
+                               dtype, q_scale_delta, k_scale_delta, scale_dtype, gate_mode, keep);
+    if (st != ME_OK) return st;
+    ME_CHECK_ARG(grad_out && row_stats && grad_hidden && grad_key && grad_value,
+                 "null gradient pointer");
+    ME_CHECK_ARG(aligned16(grad_out) && aligned16(grad_hidden) && aligned16(grad_key) &&
+                     aligned16(grad_value),
+                 "gradient tensors must be 16-byte aligned");
+    if (gate_mode == ME_GATE_SCALAR_SQRT)
+        ME_CHECK_ARG(grad_q_scale && grad_k_scale, "scalar_sqrt needs the scale gradient outputs");
+    const GradLayout l = grad_layout(n, model_dim);
+    if (workspace == nullptr || workspace_size < l.total) {
+        set_error("me_gate_backward: workspace of %zu bytes needed, got %zu", l.total, workspace_size);
+        return ME_ERR_WORKSPACE;
+    }
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    a.grad_out = static_cast<const uint8_t *>(grad_out);
+    a.row_stats = row_stats;
+    a.grad_hidden = static_cast<uint8_t *>(grad_hidden);
+    a.grad_partials = reinterpret_cast<float *>(ws + l.partials);
+    a.tok_coef = reinterpret_cast<float *>(ws + l.coef);
+    a.col_partials = reinterpret_cast<float *>(ws + l.cols);
+
+    hipStream_t s = as_stream(stream);
+    // value side (W_V, writes dV and the per-token sums of g . V), the per-token coefficients,
+    // key side (W_K, writes d hidden and dK), then the scale gradients
+    GateArgs av = a, ak = a;
+    av.w = static_cast<const uint8_t *>(w_value);
+    av.grad_proj = static_cast<uint8_t *>(grad_value);
+    ak.w = static_cast<const uint8_t *>(w_key);
+    ak.grad_proj = static_cast<uint8_t *>(grad_key);
+    const dim3 grid(static_cast<unsigned>(a.per_xcd * kXcds));
+    const dim3 tok_grid(static_cast<unsigned>(ceil_div(n, kThreads)));
+#define ME_GATE_GRAD_LAUNCH(T, H)                                                                \
+    do {                                                                                         \
+        hipLaunchKernelGGL((gate_kernel<T, H, kGradValue, false>), grid, dim3(kThreads), 0, s, av); \
+        int st_ = check_launch("me_gate_backward (value side)");                                \
+        if (st_ != ME_OK) return st_;                                                            \
+        hipLaunchKernelGGL(gate_grad_token_kernel, tok_grid, dim3(kThreads), 0, s, a);           \
+        st_ = check_launch("me_gate_backward (token coefficients)");                             \
+        if (st_ != ME_OK) return st_;                                                            \
+        hipLaunchKernelGGL((gate_kernel<T, H, kGradKey, false>), grid, dim3(kThreads), 0, s, ak); \
+        st_ = check_launch("me_gate_backward (key side)");                                       \
+        if (st_ != ME_OK) return st_;                                                            \
+    } while (0)
+    if (dtype == ME_BF16) {
+        if (hidden_dtype == ME_BF16)
+            ME_GATE_GRAD_LAUNCH(uint16_t, uint16_t);
+        else
+            ME_GATE_GRAD_LAUNCH(uint16_t, float);
+    } else {
+        if (hidden_dtype == ME_BF16)
+            ME_GATE_GRAD_LAUNCH(float, uint16_t);
+        else
+            ME_GATE_GRAD_LAUNCH(float, float);
+    }
+#undef ME_GATE_GRAD_LAUNCH
+    if (gate_mode != ME_GATE_SCALAR_SQRT) return ME_OK;
+    hipLaunchKernelGGL(gate_grad_scale_kernel,
+                       dim3(static_cast<unsigned>(ceil_div(model_dim, kThreads))), dim3(kThreads), 0, s,
+                       a, grad_q_scale, grad_k_scale);
+    return check_launch("me_gate_backward (scale gradients)");
 }

@@ -13,8 +13,11 @@ Differences from the reference, all deliberate:
     lookup + cat), then one gate/residual op.
   * lookup() returns views into one concatenated [N, n_tables * D] buffer instead of separate
     tensors per table (same values).
-  * The HIP forward has no autograd formula yet: calling it where a gradient would be needed
-    raises instead of silently detaching. Use torch.no_grad() / torch.inference_mode().
+  * Where a gradient is needed (grad mode on and hidden or a parameter requiring it), the
+    forward keeps the memory vectors and per-token gate sums, and the backward runs the HIP
+    gate backward (the projections recomputed on MFMA) plus four plain GEMMs for the weight and
+    memory gradients; the table gradients go through the dedup kernel (rows.py). Without
+    gradients, hashing and the gather run fused and nothing is kept.
   * The "ple" gate keeps its parameters (so checkpoints load) but has no HIP kernel.
 """
 import weakref
@@ -47,6 +50,41 @@ def _row_range(n_rows, rank, world):
     per = -(-n_rows // world)
     start = min(rank * per, n_rows)
     return start, max(0, min(per, n_rows - start))
+
+
+class _GateResidual(torch.autograd.Function):
+    """hidden + the gated projection of the memory vectors (module.py:239-261) with its
+    gradients: the HIP backward gives the gradients of hidden, of the key / value Linear
+    outputs and of the scale deltas; the Linear layers' own gradients are plain GEMMs
+    (dW = dY^T mem, dmem = dY_K W_K + dY_V W_V) on the library BLAS."""
+
+    @staticmethod
+    def forward(ctx, hidden, mem, w_key, w_value, q_delta, k_delta, gate_mode, keep):
+        out, alpha, stats = ops.gate_residual(
+            hidden, mem, w_key.detach(), w_value.detach(),
+            None if q_delta is None else q_delta.detach(),
+            None if k_delta is None else k_delta.detach(), gate_mode, keep, True, True)
+        ctx.save_for_backward(hidden, mem, w_key, w_value, q_delta, k_delta, keep, stats)
+        ctx.gate_mode = gate_mode
+        ctx.mark_non_differentiable(alpha)
+        return out, alpha
+
+    @staticmethod
+    def backward(ctx, grad_out, _grad_alpha):
+        hidden, mem, w_key, w_value, q_delta, k_delta, keep, stats = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        wk, wv = w_key.detach(), w_value.detach()
+        g_hidden, g_key, g_value, g_q, g_k = ops.gate_backward(
+            grad_out.contiguous(), hidden.detach(), mem.detach(), wk, wv,
+            None if q_delta is None else q_delta.detach(),
+            None if k_delta is None else k_delta.detach(), ctx.gate_mode, keep, stats)
+        m = mem.detach().reshape(g_key.shape[0], -1)
+        d_mem = torch.addmm(g_key @ wk, g_value, wv).reshape(mem.shape) if need[1] else None
+        d_wk = g_key.t() @ m if need[2] else None
+        d_wv = g_value.t() @ m if need[3] else None
+        d_q = g_q.to(q_delta.dtype) if need[4] else None
+        d_k = g_k.to(k_delta.dtype) if need[5] else None
+        return g_hidden if need[0] else None, d_mem, d_wk, d_wv, d_q, d_k, None, None
 
 
 class MicroEngram(nn.Module):
@@ -258,6 +296,24 @@ class MicroEngram(nn.Module):
             return torch.cat(self.row_lookup_fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
         return ops.gather(self._stacked_idx(idx), self._table_weights())
 
+    def _mem_grad(self, idx):
+        """The memory vectors [N, n_tables * D] with the tables' gradients attached: the row
+        lookup of rows.py (dense table gradients, or sparse ones for row shards so marked)."""
+        if self.row_shards is not None:
+            if self.row_lookup_fn is not None:
+                return torch.cat(self.row_lookup_fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
+            rank, world = self.row_info[0], self.row_info[1]
+            if world != 1:
+                raise NotImplementedError(
+                    f"[micro_engram] row-sharded tables over {world} ranks need the multi-GPU row "
+                    "exchange, which this single-GPU build does not provide")
+            weights = list(self.row_shards)
+        else:
+            weights = [t.weight for t in self.tables]
+        from .rows import _RowLookup, _table_offsets
+
+        return _RowLookup.apply(self._stacked_idx(idx), _table_offsets(self), *weights)
+
     def lookup(self, idx):
         """The table rows for the hashed ids: list of n_tables tensors [*idx shape, D]
         (module.py:146-154). Row-sharded tables go through the server's lookup or the
@@ -274,12 +330,9 @@ class MicroEngram(nn.Module):
         return [mem[:, k * D:(k + 1) * D].reshape(*shape, D) for k in range(len(idx))]
 
     # -------------------------------------------------------------------------------- inject
-    def _check_no_grad(self, hidden):
-        if torch.is_grad_enabled() and (hidden.requires_grad or any(
-                p.requires_grad for p in self.all_parameters())):
-            raise RuntimeError(
-                "[micro_engram] the HIP engram forward has no backward yet: run it under "
-                "torch.no_grad() / torch.inference_mode(), or freeze the engram's parameters")
+    def _needs_grad(self, hidden):
+        return torch.is_grad_enabled() and (hidden.requires_grad or any(
+            p.requires_grad for p in self.all_parameters()))
 
     def _gate(self, hidden, mem, keep):
         if self.gate not in self.SCALAR_GATES:
@@ -288,6 +341,14 @@ class MicroEngram(nn.Module):
         if mem.dtype != reader.dtype:
             mem = mem.to(reader.dtype)  # rows stored in another dtype (module.py:234-238)
         sqrt = self.gate == "scalar_sqrt"
+        mode = ME_GATE_SCALAR_SQRT if sqrt else ME_GATE_SCALAR
+        if self._needs_grad(hidden) or mem.requires_grad:
+            out, alpha = _GateResidual.apply(hidden, mem, self.key.weight, self.value.weight,
+                                             self.q_scale if sqrt else None,
+                                             self.k_scale if sqrt else None, mode, keep)
+            if self.training:
+                self._record_gate(alpha)
+            return out
         outs = ops.gate_residual(
             hidden, mem, self.key.weight.detach(), self.value.weight.detach(),
             self.q_scale.detach() if sqrt else None, self.k_scale.detach() if sqrt else None,
@@ -299,14 +360,13 @@ class MicroEngram(nn.Module):
     def inject(self, hidden, idx, keep=None):
         """hidden + gated memory of the rows `idx` (module.py:228-261); keep: optional [N] bool,
         False leaves that token unchanged. Returns a new tensor."""
-        self._check_no_grad(hidden)
-        return self._gate(hidden, self._mem(idx), keep)
+        mem = self._mem_grad(idx) if self._needs_grad(hidden) else self._mem(idx)
+        return self._gate(hidden, mem, keep)
 
     def forward(self, hidden, input_ids, position_ids=None):
-        """inject(hidden, hash_ids(input_ids, position_ids)) with hashing and gather fused into
-        one kernel (module.py:263-265)."""
-        self._check_no_grad(hidden)
-        if self.row_lookup_fn is not None and self.row_shards is not None:
+        """inject(hidden, hash_ids(input_ids, position_ids)) (module.py:263-265); without
+        gradients the hashing and the gather run as one fused kernel."""
+        if self._needs_grad(hidden) or (self.row_lookup_fn is not None and self.row_shards is not None):
             return self.inject(hidden, self.hash_ids(input_ids.to(hidden.device), position_ids))
         return self._gate(hidden, self.hashed_memory(input_ids, position_ids, hidden.device), None)
 
@@ -322,7 +382,6 @@ class MicroEngram(nn.Module):
 
     def gate_residual(self, hidden, mem, keep=None):
         """hidden + the gated projection of the memory vectors `mem` (module.py:239-261)."""
-        self._check_no_grad(hidden)
         return self._gate(hidden, mem, keep)
 
     # ------------------------------------------------------------------------- gate statistics

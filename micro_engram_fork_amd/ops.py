@@ -242,15 +242,8 @@ def _aligned(t):
     return t.data_ptr() % 16 == 0
 
 
-@torch.library.custom_op("micro_engram_amd::gate_residual", mutates_args=())
-def gate_residual(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
-                  w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
-                  k_scale_delta: Optional[torch.Tensor], gate_mode: int,
-                  keep: Optional[torch.Tensor], with_alpha: bool) -> List[torch.Tensor]:
-    """[out] or [out, alpha [N] fp32]: hidden + gated W_V mem, the scalar gates of
-    MicroEngram.inject (micro_engram/module.py:239-261). hidden [..., d]; mem [N, M] with N the
-    number of hidden rows; weights [d, M] (nn.Linear layout) in mem's dtype."""
-    dev = require_gpu(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, keep)
+def _gate_operands(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep):
+    """Checked, contiguous, 16-byte aligned operands of the gate kernels."""
     d = hidden.shape[-1]
     x = hidden.reshape(-1, d)
     N = x.shape[0]
@@ -272,29 +265,106 @@ def gate_residual(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
         q_scale_delta, k_scale_delta = q_scale_delta.contiguous(), k_scale_delta.contiguous()
         if q_scale_delta.dtype != k_scale_delta.dtype:
             k_scale_delta = k_scale_delta.to(q_scale_delta.dtype)
+        if not (_aligned(q_scale_delta) and _aligned(k_scale_delta)):
+            q_scale_delta, k_scale_delta = q_scale_delta.clone(), k_scale_delta.clone()
         scale_code = dtype_code(q_scale_delta)
     keep_u8 = None
     if keep is not None:
         keep_u8 = keep.reshape(-1).to(torch.uint8).contiguous()
         if keep_u8.numel() != N:
             raise ValueError(f"[micro_engram] keep has {keep_u8.numel()} entries for {N} tokens")
+    return x, mem, w_key, w_value, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M
+
+
+@torch.library.custom_op("micro_engram_amd::gate_residual", mutates_args=())
+def gate_residual(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
+                  w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
+                  k_scale_delta: Optional[torch.Tensor], gate_mode: int,
+                  keep: Optional[torch.Tensor], with_alpha: bool,
+                  with_stats: bool = False) -> List[torch.Tensor]:
+    """[out], plus alpha [N] fp32 when with_alpha, plus row stats [N, 4] fp32 (what the backward
+    needs) when with_stats: hidden + gated W_V mem, the scalar gates of MicroEngram.inject
+    (micro_engram/module.py:239-261). hidden [..., d]; mem [N, M] with N the number of hidden
+    rows; weights [d, M] (nn.Linear layout) in mem's dtype."""
+    dev = require_gpu(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, keep)
+    x, mem, w_key, w_value, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M = \
+        _gate_operands(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep)
     out = torch.empty_like(x)
     alpha = torch.empty(N, dtype=torch.float32, device=dev) if with_alpha else None
+    stats = torch.empty((N, 4), dtype=torch.float32, device=dev) if with_stats else None
     ws = torch.empty(max(gate_workspace_bytes(N, d), 16), dtype=torch.uint8, device=dev)
     call("me_gate_residual", x.data_ptr(), dtype_code(x), N, d, mem.data_ptr(), M,
          w_key.data_ptr(), w_value.data_ptr(), dtype_code(mem), _p(q_scale_delta),
          _p(k_scale_delta), scale_code, gate_mode, _p(keep_u8), out.data_ptr(), _p(alpha),
-         ws.data_ptr(), ws.numel(), stream_of(dev))
-    out = out.reshape(hidden.shape)
-    return [out, alpha] if with_alpha else [out]
+         _p(stats), ws.data_ptr(), ws.numel(), stream_of(dev))
+    res = [out.reshape(hidden.shape)]
+    if with_alpha:
+        res.append(alpha)
+    if with_stats:
+        res.append(stats)
+    return res
 
 
 @gate_residual.register_fake
-def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha):
-    out = torch.empty_like(hidden)
+def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha,
+      with_stats=False):
+    n = hidden.numel() // hidden.shape[-1]
+    res = [torch.empty_like(hidden)]
     if with_alpha:
-        return [out, hidden.new_empty((hidden.numel() // hidden.shape[-1],), dtype=torch.float32)]
-    return [out]
+        res.append(hidden.new_empty((n,), dtype=torch.float32))
+    if with_stats:
+        res.append(hidden.new_empty((n, 4), dtype=torch.float32))
+    return res
+
+
+def gate_backward_workspace_bytes(n, d):
+    size = ctypes.c_size_t(0)
+    call("me_gate_backward_workspace_size", n, d, ctypes.byref(size))
+    return size.value
+
+
+@torch.library.custom_op("micro_engram_amd::gate_backward", mutates_args=())
+def gate_backward(grad_out: torch.Tensor, hidden: torch.Tensor, mem: torch.Tensor,
+                  w_key: torch.Tensor, w_value: torch.Tensor,
+                  q_scale_delta: Optional[torch.Tensor], k_scale_delta: Optional[torch.Tensor],
+                  gate_mode: int, keep: Optional[torch.Tensor],
+                  stats: torch.Tensor) -> List[torch.Tensor]:
+    """Gradients of gate_residual from the gradient of its output: [grad_hidden (like hidden),
+    grad_key [N, d] and grad_value [N, d] (gradients of the key / value Linear outputs, in
+    mem's dtype), grad_q_scale_delta, grad_k_scale_delta ([d] fp32; empty for the scalar
+    gate)] -- what autograd gives through module.py:239-261."""
+    dev = require_gpu(grad_out, hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, keep,
+                      stats)
+    x, mem, w_key, w_value, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M = \
+        _gate_operands(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep)
+    g = grad_out.reshape(-1, d).to(x.dtype).contiguous()
+    if not _aligned(g):
+        g = g.clone()
+    stats = stats.contiguous()
+    if tuple(stats.shape) != (N, 4) or stats.dtype != torch.float32:
+        raise ValueError(f"[micro_engram] stats must be fp32 [{N}, 4], got {tuple(stats.shape)}")
+    grad_hidden = torch.empty_like(x)
+    grad_key = torch.empty((N, d), dtype=mem.dtype, device=dev)
+    grad_value = torch.empty((N, d), dtype=mem.dtype, device=dev)
+    sqrt = gate_mode == _lib.ME_GATE_SCALAR_SQRT
+    grad_q = torch.empty(d if sqrt else 0, dtype=torch.float32, device=dev)
+    grad_k = torch.empty(d if sqrt else 0, dtype=torch.float32, device=dev)
+    ws = torch.empty(max(gate_backward_workspace_bytes(N, d), 16), dtype=torch.uint8, device=dev)
+    call("me_gate_backward", x.data_ptr(), dtype_code(x), N, d, mem.data_ptr(), M,
+         w_key.data_ptr(), w_value.data_ptr(), dtype_code(mem), _p(q_scale_delta),
+         _p(k_scale_delta), scale_code, gate_mode, _p(keep_u8), g.data_ptr(), stats.data_ptr(),
+         grad_hidden.data_ptr(), grad_key.data_ptr(), grad_value.data_ptr(),
+         grad_q.data_ptr() if sqrt else None, grad_k.data_ptr() if sqrt else None, ws.data_ptr(),
+         ws.numel(), stream_of(dev))
+    return [grad_hidden.reshape(hidden.shape), grad_key, grad_value, grad_q, grad_k]
+
+
+@gate_backward.register_fake
+def _(grad_out, hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep, stats):
+    n, d = hidden.numel() // hidden.shape[-1], hidden.shape[-1]
+    nd = d if gate_mode == _lib.ME_GATE_SCALAR_SQRT else 0
+    return [torch.empty_like(hidden), mem.new_empty((n, d)), mem.new_empty((n, d)),
+            hidden.new_empty((nd,), dtype=torch.float32), hidden.new_empty((nd,), dtype=torch.float32)]
 
 
 def library_loaded():

@@ -16,6 +16,9 @@ inject                   micro_engram/module.py:228-261                   closed
                                                                           value=0 no-op and keep-mask
                                                                           cases of test_gate.py:24-27,
                                                                           122-130
+inject_backward          autograd of micro_engram/module.py:239-261       torch.autograd of inject on the
+                         (closed form, float64)                           same inputs; finite differences
+                                                                          of inject in float64
 dedup                    micro_engram/rows.py:81, 117-118, 137-147        brute-force Python loop on tiny
                                                                           inputs; uniq[inv] == keys
 philox4x32_10            Salmon et al. 2011 (Random123)                   published known-answer vectors
@@ -173,24 +176,73 @@ def inject(hidden, mem, w_key, w_value, gate="scalar_sqrt", q_scale_delta=None, 
     hidden [N, d] (bf16 or fp32); mem [N, M] and w_key/w_value [d, M] in the engram's dtype;
     the scale deltas are the stored q_scale/k_scale parameters (scale - 1, module.py:156-164)."""
     d = hidden.shape[-1]
+    # the reference's .float(): bf16 / fp32 -> fp32; float64 inputs (the backward's pinning
+    # tests) stay float64
+    up = lambda t: t.to(torch.promote_types(t.dtype, torch.float32))
+    eps = torch.finfo(torch.float32).eps  # rms_norm's default for the reference's fp32 math
     if gate == "scalar_sqrt":
-        q_scale, k_scale = 1 + q_scale_delta.float(), 1 + k_scale_delta.float()
-        h = F.rms_norm(hidden.float(), (d,), weight=q_scale)
-        k = F.rms_norm(F.linear(mem, w_key).float(), (d,), weight=k_scale)
+        q_scale, k_scale = 1 + up(q_scale_delta), 1 + up(k_scale_delta)
+        h = F.rms_norm(up(hidden), (d,), weight=q_scale, eps=eps)
+        k = F.rms_norm(up(F.linear(mem, w_key)), (d,), weight=k_scale, eps=eps)
     elif gate == "scalar":
-        h = F.rms_norm(hidden.float(), (d,))
-        k = F.rms_norm(F.linear(mem, w_key).float(), (d,))
+        h = F.rms_norm(up(hidden), (d,), eps=eps)
+        k = F.rms_norm(up(F.linear(mem, w_key)), (d,), eps=eps)
     else:
         raise ValueError(f"gate {gate!r} is not on this path")
     s = (h * k).sum(-1, keepdim=True) / d ** 0.5
     if gate == "scalar_sqrt":
         s = s.sign() * s.abs().clamp_min(1e-6).sqrt()
     alpha = torch.sigmoid(s)
-    out = alpha * F.linear(mem, w_value).float()
+    out = alpha * up(F.linear(mem, w_value))
     if keep is not None:
         out = out * keep.reshape(*out.shape[:-1], 1).to(out.dtype)
     res = hidden + out.to(hidden.dtype)
     return (res, alpha.reshape(-1)) if return_alpha else res
+
+
+def inject_backward(grad_out, hidden, mem, w_key, w_value, gate="scalar_sqrt", q_scale_delta=None,
+                    k_scale_delta=None, keep=None):
+    """Closed-form gradients of inject (module.py:239-261) in float64, from the gradient of its
+    output: (d hidden, d K, d V, d q_scale_delta, d k_scale_delta), with K = W_K mem and V = W_V
+    mem the key / value Linear outputs (their weight and mem gradients are the plain products
+    dK^T mem, dV^T mem, dK W_K + dV W_V). No dtype roundings: the float64 formula itself.
+
+    Per token, with r_h = rsqrt(mean x^2 + eps), r_k = rsqrt(mean K^2 + eps), w = qs * ks,
+    sck = sum x w K, s0 = r_h r_k sck / sqrt(d), alpha = sigmoid(s):
+      dV = alpha keep g;  d alpha = keep sum g V;  ds = d alpha alpha (1 - alpha)
+      ds0 = ds / (2 sqrt|s0|) if |s0| >= 1e-6 else 0 (scalar_sqrt; the scalar gate: ds0 = ds)
+      a = ds0 r_h r_k / sqrt(d)
+      d hidden = g + a (w K - x r_h^2 sck / d);  dK = a (w x - K r_k^2 sck / d)
+      d q_scale_j = ks_j sum_tokens a x_j K_j;  d k_scale_j = qs_j sum_tokens a x_j K_j"""
+    f = lambda t: t.detach().double()
+    x, e, g = f(hidden), f(mem), f(grad_out)
+    d = x.shape[-1]
+    eps = float(torch.finfo(torch.float32).eps)
+    K, V = e @ f(w_key).T, e @ f(w_value).T
+    if gate == "scalar_sqrt":
+        qs, ks = 1 + f(q_scale_delta), 1 + f(k_scale_delta)
+    else:
+        qs = ks = torch.ones(d, dtype=torch.float64)
+    w = qs * ks
+    rh = 1.0 / torch.sqrt((x * x).mean(-1) + eps)
+    rk = 1.0 / torch.sqrt((K * K).mean(-1) + eps)
+    sck = (x * w * K).sum(-1)
+    s0 = rh * rk * sck / d ** 0.5
+    s = s0.sign() * s0.abs().clamp_min(1e-6).sqrt() if gate == "scalar_sqrt" else s0
+    alpha = torch.sigmoid(s)
+    kf = torch.ones_like(alpha) if keep is None else f(keep.reshape(-1).to(torch.float64))
+    dV = (alpha * kf)[:, None] * g
+    dalpha = kf * (g * V).sum(-1)
+    ds = dalpha * alpha * (1 - alpha)
+    if gate == "scalar_sqrt":
+        ds0 = torch.where(s0.abs() >= 1e-6, ds / (2 * s0.abs().clamp_min(1e-6).sqrt()), torch.zeros_like(ds))
+    else:
+        ds0 = ds
+    a = ds0 * rh * rk / d ** 0.5
+    dx = g + a[:, None] * (w * K - x * (rh * rh * sck / d)[:, None])
+    dK = a[:, None] * (w * x - K * (rk * rk * sck / d)[:, None])
+    P = (a[:, None] * x * K).sum(0)
+    return dx, dK, dV, ks * P, qs * P
 
 
 # ------------------------------------------------------------------------------------- dedup

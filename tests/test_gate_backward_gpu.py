@@ -1,0 +1,178 @@
+"""Backward of the engram (stages 2-3) on the GPU against torch autograd of the oracle's CPU
+restatement of MicroEngram.inject (module.py:228-261) with nn.Embedding-style lookups: the
+gradients of hidden, of the key / value weights, of the q/k scale deltas and of the tables.
+
+Tolerances (per gradient tensor, relative to the reference's largest entry):
+  fp32  max |gpu - ref| <= 1e-4 * max |ref|   (fp32 GEMM and reduction orders differ)
+  bf16  max |gpu - ref| <= 4e-2 * max |ref| and ||gpu - ref|| <= 1e-2 ||ref||: the products
+        K, V and the gradients dK, dV are rounded to bf16 on both sides, and one-ulp flips of
+        those roundings between the two accumulation orders move individual entries
+The step-0 properties of test_gate.py:24-44 are exact.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from micro_engram_fork_amd import MicroEngram, synthetic
+from micro_engram_fork_amd.rows import RowTables
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _make(dtype, gate, d, dim, heads, orders=(2, 3, 4), seed=0, std=0.2):
+    eng = MicroEngram(model_dim=d, table_size=257, engram_dim=dim, num_heads=heads, orders=orders,
+                      table_sizes={2: 131, 3: 257, 4: 97}, vocab_size=1000, gate=gate, seed=seed)
+    synthetic.fill_dense(eng, seed=seed, std=std)
+    return eng.to(device=DEV, dtype=dtype)
+
+
+def _reference_grads(eng, hidden, ids, grad_out, keep=None):
+    """torch autograd on the CPU of the oracle's inject over nn.Embedding lookups."""
+    idx = [i.cpu() for i in eng.hash_ids(ids)]
+    leaf = lambda t: t.detach().cpu().clone().requires_grad_(True)
+    tables = [leaf(t.weight) for t in eng.tables]
+    wk, wv = leaf(eng.key.weight), leaf(eng.value.weight)
+    sqrt = eng.gate == "scalar_sqrt"
+    dq = leaf(eng.q_scale) if sqrt else None
+    dk = leaf(eng.k_scale) if sqrt else None
+    h = leaf(hidden)
+    d = hidden.shape[-1]
+    mem = torch.cat([F.embedding(i.reshape(-1), t) for i, t in zip(idx, tables)], dim=-1)
+    out = oracle.inject(h.reshape(-1, d), mem, wk, wv, eng.gate, dq, dk,
+                        keep=None if keep is None else keep.cpu().reshape(-1))
+    out.backward(grad_out.cpu().reshape(-1, d).to(out.dtype))
+    grads = {"hidden": h.grad, "key": wk.grad, "value": wv.grad}
+    if sqrt:
+        grads["q_scale"], grads["k_scale"] = dq.grad, dk.grad
+    for k, t in enumerate(tables):
+        grads[f"table{k}"] = t.grad
+    return out.detach(), grads
+
+
+def _conditioned(eng, hidden, ids, grad_out, keep=None):
+    """grad_out with the rows of tokens whose scalar_sqrt score is near 0 zeroed: there
+    d sqrt|s0| / d s0 = 1 / (2 sqrt|s0|) amplifies the fp32 rounding of s0 itself (a sum of
+    O(sqrt d) magnitude), so no two evaluation orders agree on those tokens' gradients. With
+    |s| = sqrt|s0| >= 0.1 the amplification stays below ~1e-4 relative."""
+    if eng.gate != "scalar_sqrt":
+        return grad_out
+    idx = [i.cpu() for i in eng.hash_ids(ids)]
+    d = hidden.shape[-1]
+    mem = torch.cat([F.embedding(i.reshape(-1), t.weight.detach().cpu()) for i, t in zip(idx, eng.tables)], -1)
+    _, alpha = oracle.inject(hidden.cpu().reshape(-1, d), mem, eng.key.weight.detach().cpu(),
+                             eng.value.weight.detach().cpu(), eng.gate, eng.q_scale.detach().cpu(),
+                             eng.k_scale.detach().cpu(), return_alpha=True)
+    s = torch.log(alpha / (1 - alpha))
+    ok = (s.abs() >= 0.1).to(grad_out.dtype).to(grad_out.device)
+    return grad_out * ok.reshape(*grad_out.shape[:-1], 1)
+
+
+def _gpu_grads(eng, hidden, ids, grad_out, keep=None):
+    eng.zero_grad(set_to_none=True)
+    h = hidden.detach().clone().requires_grad_(True)
+    if keep is None:
+        out = eng(h, ids)
+    else:
+        out = eng.inject(h, eng.hash_ids(ids), keep=keep)
+    out.backward(grad_out)
+    grads = {"hidden": h.grad, "key": eng.key.weight.grad, "value": eng.value.weight.grad}
+    if eng.gate == "scalar_sqrt":
+        grads["q_scale"], grads["k_scale"] = eng.q_scale.grad, eng.k_scale.grad
+    for k, t in enumerate(eng.tables):
+        grads[f"table{k}"] = t.weight.grad
+    return out.detach(), grads
+
+
+def _assert_grads_close(got, want, dtype):
+    assert set(got) == set(want)
+    for name in want:
+        g, w = got[name].float().cpu(), want[name].float()
+        assert g.shape == w.shape, name
+        scale = float(w.abs().max())
+        err = (g - w).abs()
+        if dtype == torch.float32:
+            assert float(err.max()) <= 1e-4 * scale + 1e-12, (name, float(err.max()), scale)
+        else:
+            assert float(err.max()) <= 4e-2 * scale + 1e-12, (name, float(err.max()), scale)
+            assert float((g - w).norm()) <= 1e-2 * float(w.norm()) + 1e-12, (name, float((g - w).norm()))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("gate", ["scalar_sqrt", "scalar"])
+@pytest.mark.parametrize("n,d,dim,heads", [(300, 264, 8, 3), (600, 520, 16, 4)])
+def test_backward_matches_autograd(dtype, gate, n, d, dim, heads):
+    torch.manual_seed(n + d)
+    eng = _make(dtype, gate, d, dim, heads).train()
+    ids = torch.randint(0, 1000, (1, n), device=DEV)
+    hidden = (torch.randn(1, n, d) * 3).to(dtype).to(DEV)
+    grad_out = _conditioned(eng, hidden, ids, torch.randn(1, n, d).to(dtype).to(DEV))
+    out, got = _gpu_grads(eng, hidden, ids, grad_out)
+    ref_out, want = _reference_grads(eng, hidden, ids, grad_out)
+    _assert_grads_close(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_with_keep(dtype):
+    torch.manual_seed(3)
+    eng = _make(dtype, "scalar_sqrt", 136, 8, 2).train()
+    n = 260
+    ids = torch.randint(0, 1000, (1, n), device=DEV)
+    hidden = torch.randn(1, n, 136).to(dtype).to(DEV)
+    grad_out = _conditioned(eng, hidden, ids, torch.randn(1, n, 136).to(dtype).to(DEV))
+    keep = torch.rand(n, device=DEV) > 0.4
+    _, got = _gpu_grads(eng, hidden, ids, grad_out, keep=keep)
+    _, want = _reference_grads(eng, hidden, ids, grad_out, keep=keep)
+    _assert_grads_close(got, want, dtype)
+    # tokens without memory pass the output gradient straight through
+    assert torch.equal(got["hidden"][0][~keep], grad_out[0][~keep])
+
+
+def test_step0_gradients():
+    # test_gate.py:24-44: with the zero-init value layer the output is hidden, only the value
+    # layer gets a gradient; once it is non-zero, the tables learn too
+    for dtype in (torch.float32, torch.bfloat16):
+        eng = MicroEngram(model_dim=32, table_size=257, engram_dim=4, num_heads=2, vocab_size=1000,
+                          gate="scalar_sqrt").to(device=DEV, dtype=dtype).train()
+        ids = torch.randint(5, 1000, (2, 12), device=DEV)
+        hidden = (torch.randn(2, 12, 32) * 50).to(dtype).to(DEV).requires_grad_(True)
+        out = eng(hidden, ids)
+        assert torch.equal(out, hidden)
+        g = torch.randn_like(out)
+        out.backward(g)
+        assert torch.equal(hidden.grad, g)
+        assert eng.value.weight.grad.abs().sum() > 0
+        assert not eng.key.weight.grad.any() and not eng.q_scale.grad.any()
+        assert all(not t.weight.grad.any() for t in eng.tables)
+        eng.zero_grad()
+        with torch.no_grad():
+            eng.value.weight.normal_(std=0.02)
+        eng(hidden.detach(), ids).pow(2).sum().backward()
+        assert eng.tables[0].weight.grad.abs().sum() > 0
+        assert eng.q_scale.grad.abs().sum() > 0 and eng.k_scale.grad.abs().sum() > 0
+
+
+def test_sparse_row_gradients_equal_dense():
+    # row shards at world size 1 with sparse gradients (rows.py:137-147): the coalesced
+    # (rows, fp32 sums) equal the dense table gradient's non-zero rows
+    torch.manual_seed(9)
+    dense = _make(torch.float32, "scalar_sqrt", 64, 8, 2).train()
+    sparse = _make(torch.float32, "scalar_sqrt", 64, 8, 2).train()
+    sparse.load_state_dict(dense.state_dict())
+    sparse.shard_rows(0, 1)
+    rt = RowTables([("e", sparse)], lazy=True, rowwise=True, sparse_grads=True)
+    ids = torch.randint(0, 1000, (2, 100), device=DEV)
+    hidden = torch.randn(2, 100, 64, device=DEV)
+    g = torch.randn(2, 100, 64, device=DEV)
+    dense(hidden, ids).backward(g)
+    sparse(hidden, ids).backward(g)
+    for t, shard in zip(dense.tables, sparse.row_shards):
+        rows, sums = shard.sparse_grad
+        want = t.weight.grad
+        nz = want.abs().sum(-1).nonzero().reshape(-1)
+        assert torch.equal(torch.sort(rows).values, rows)
+        assert set(nz.tolist()) <= set(rows.tolist())
+        assert torch.equal(sums, want[rows])
+    assert torch.equal(dense.key.weight.grad, sparse.key.weight.grad)
+    rt.zero_grad()

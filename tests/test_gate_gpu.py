@@ -138,10 +138,17 @@ def test_gate_stats_recorded_in_training_mode():
     assert eng.pop_gate_stats() is None
 
 
-def test_grad_mode_raises():
-    eng = _make(torch.float32)
-    with pytest.raises(RuntimeError, match="no backward"):
-        eng(torch.randn(1, 4, 32, device=DEV), torch.randint(0, 1000, (1, 4), device=DEV))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_grad_path_forward_equals_fused(dtype):
+    # with gradients the forward hashes, gathers through the differentiable row lookup and
+    # keeps the gate's row sums; its output is the fused inference forward's, bit for bit
+    eng = _make(dtype, d=64, dim=8, heads=2, orders=(2, 3, 4)).train()
+    ids = torch.randint(0, 1000, (2, 70), device=DEV)
+    hidden = torch.randn(2, 70, 64).to(dtype).to(DEV)
+    with torch.no_grad():
+        fused = eng(hidden, ids)
+    out = eng(hidden.clone().requires_grad_(True), ids)
+    assert out.requires_grad and torch.equal(out.detach(), fused)
 
 
 def test_golden_inject_fixture():
