@@ -51,11 +51,11 @@ def parse():
     return ap.parse_args()
 
 
-# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,100.2
-# KiB per dispatch, x2.0) and WRITE_SIZE (24,580.9 KiB, x1.0), the factors being what the two
+# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,104.5
+# KiB per dispatch, x2.0) and WRITE_SIZE (24,586.4 KiB, x1.0), the factors being what the two
 # counters read for this script's 1 GiB device copy. A counter run cannot share a process with
 # the timing, so the figure is a measured constant, re-measured when the kernel changes.
-GATHER_TRAFFIC_BYTES = 49_951_520
+GATHER_TRAFFIC_BYTES = 49_966_464
 CYCLE = 16  # distinct prefill batches the timed steps cycle through
 
 
