@@ -8,10 +8,15 @@ the radix-sort dedup kernel here (bit-exact: same unique keys, inverse and fp32 
 keep them per table as p.sparse_grad = (unique rows, fp32 sums) (rows.py:137-147). More than one
 rank needs that exchange, which this single-GPU build does not provide; it raises.
 """
+import os
+
 import torch
 
 from . import ops
 from .optim import LazyAdamW
+
+ROWS_DIR = "micro_engram_rows"              # complete engram (tables + the rest), DCP (rows.py:27)
+ROWS_OPTIM_DIR = "micro_engram_rows_optim"  # the tables' optimizer state, DCP (rows.py:28)
 
 
 def row_range(n_rows, rank, world):
@@ -161,8 +166,105 @@ class RowTables:
         for p in self.params():
             p.sparse_grad = None
 
+    # --- checkpoints (DCP folders the reference's loaders and RowTables.load read) ---
+    def _table_items(self, frozen_too=False):
+        """(full name of table k, rows, row shard) of every engram with trainable rows."""
+        for prefix, e in self.entries:
+            if not frozen_too and not any(p.requires_grad for p in e.row_shards):
+                continue
+            for k, p in enumerate(e.row_shards):
+                yield f"{prefix}tables.{k}.weight", e.table_rows[k], p
+
     def save(self, folder, optim_folder=None):
-        raise NotImplementedError("[micro_engram] DCP checkpoints of the row tables are not part of this build")
+        """The complete engrams (tables + key/value/scales/buffers under their full names) to the
+        DCP folder `folder`, and the tables' optimizer state (exp_avg, exp_avg_sq, step per
+        table) to `optim_folder` (rows.py:258-281). Engrams whose rows are frozen are skipped.
+        On one GPU every shard is its whole table, so the tensors are written as they are."""
+        import torch.distributed.checkpoint as dcp
+
+        sd = {}
+        for prefix, e in self.entries:
+            if any(p.requires_grad for p in e.row_shards):
+                sd.update({prefix + k: v.detach() for k, v in e.state_dict().items()})
+        for key, _rows, p in self._table_items():
+            sd[key] = p.detach()
+        if sd:
+            dcp.save(sd, checkpoint_id=folder, no_dist=True)
+        if optim_folder and self.optimizer is not None:
+            osd = {}
+            for key, _rows, p in self._table_items():
+                st = self.optimizer.state.get(p)
+                if st:
+                    osd[f"{key}.exp_avg"] = st["exp_avg"]
+                    osd[f"{key}.exp_avg_sq"] = st["exp_avg_sq"]
+                    osd[f"{key}.step"] = st["step"].detach().clone().reshape(())
+            if osd:
+                dcp.save(osd, checkpoint_id=optim_folder, no_dist=True)
 
     def load(self, folder, optim_folder=None):
-        raise NotImplementedError("[micro_engram] DCP checkpoints of the row tables are not part of this build")
+        """Tables from a DCP folder (a micro_engram_rows folder, or an FSDP checkpoint of a run
+        without row sharding), read into the row shards in place; optimizer state from
+        optim_folder when it exists, the second moment converted when it was saved by the other
+        optimizer (per value <-> per row). Returns (tables loaded, optimizer state loaded)
+        (rows.py:283-343)."""
+        import torch.distributed.checkpoint as dcp
+
+        from .weights import layer_of_key, local_name
+
+        meta = dcp.FileSystemReader(folder).read_metadata().state_dict_metadata
+        by_name = {}
+        for k in meta:
+            local = local_name(k)
+            if local is not None and local.startswith("tables."):
+                by_name[(layer_of_key(k), local)] = k
+        want = {}
+        for prefix, e in self.entries:
+            layer = layer_of_key(prefix + "x")
+            for k, p in enumerate(e.row_shards):
+                name = f"tables.{k}.weight"
+                found = by_name.get((layer, name)) or by_name.get((None, name))
+                if found is None:
+                    raise ValueError(f"[micro_engram] {folder} has no {name} for {prefix.rstrip('.')}")
+                saved_rows = meta[found].size[0]
+                if saved_rows != e.table_rows[k]:
+                    raise ValueError(f"[micro_engram] {folder}: {name} has {saved_rows:,} rows, this engram's "
+                                     f"table {k} (order {e._table_orders[k]}) has {e.table_rows[k]:,}: "
+                                     f"different table sizes can't resume (start a new run, or keep the sizes)")
+                want[found] = p
+        dcp.load({k: p.data for k, p in want.items()}, checkpoint_id=folder, no_dist=True)
+        self.converted = 0
+        if not (optim_folder and self.optimizer is not None and os.path.isdir(optim_folder)):
+            return len(want), False
+        ometa = dcp.FileSystemReader(optim_folder).read_metadata().state_dict_metadata
+        templ, steps, convert = {}, {}, {}
+        group = self.optimizer.param_groups[0]
+        for key, _rows, p in self._table_items():
+            if f"{key}.exp_avg" not in ometa:
+                continue
+            st = self.optimizer.state[p]
+            if not st:
+                LazyAdamW.init_state(st, p, group)
+            templ[f"{key}.exp_avg"] = st["exp_avg"]
+            saved_dims = len(ometa[f"{key}.exp_avg_sq"].size)
+            sq = st["exp_avg_sq"]
+            if saved_dims != sq.dim():  # written by the other optimizer (lazy <-> rowwise)
+                sq = torch.zeros(p.shape if saved_dims == p.dim() else p.shape[:1], dtype=torch.float32,
+                                 device=p.device)
+                convert[p] = sq
+            templ[f"{key}.exp_avg_sq"] = sq
+            templ[f"{key}.step"] = steps[p] = torch.zeros((), dtype=torch.float32)
+        if not templ:
+            return len(want), False
+        dcp.load(templ, checkpoint_id=optim_folder, no_dist=True)
+        for p, s in steps.items():
+            self.optimizer.state[p]["step"] = s
+        for p, sq in convert.items():
+            st = self.optimizer.state[p]
+            if sq.dim() > st["exp_avg_sq"].dim():
+                # per value -> per row: v is linear in g^2, so the row mean of the per-value
+                # moments is exactly the row-wise moment
+                st["exp_avg_sq"].copy_(sq.flatten(1).mean(dim=1))
+            else:  # per row -> per value: every value of the row takes the row's moment
+                st["exp_avg_sq"].copy_(sq.reshape(-1, *([1] * (p.dim() - 1))).expand_as(p))
+        self.converted = len(convert)
+        return len(want), True
