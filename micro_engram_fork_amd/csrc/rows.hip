@@ -19,6 +19,7 @@
 // of CPU index_add_.
 #include "me_common.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace me {
@@ -283,6 +284,436 @@ __global__ __launch_bounds__(kThreads) void seg_sum(const G *grads, uint32_t dim
         *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     else
         out[0] = acc[0];
+}
+
+// ---- bucket dedup -----------------------------------------------------------------------------
+// The dedup when keys fit 32 bits below a bucket: every (key, position) goes to the bucket of
+// its high key bits (key >> shift, ~24 keys per bucket on average), one workgroup per bucket
+// sorts the bucket's (low key bits, position) composites -- distinct because positions are, so
+// their order is the stable order of the keys -- and counts its unique keys, and one workgroup
+// per bucket writes the unique keys, the inverse and the segments (in the layout seg_sum reads)
+// numbered after the earlier buckets' unique keys. Five launches in place of two per 8-bit
+// digit of a radix sort, and no device-scope atomics on hot counters (they cost tens of
+// microseconds here): per-tile histograms in LDS, a [tile][bucket] matrix of counts and a
+// prefix over it, and the scatter's slots from LDS counters seeded with each tile's bases.
+// Buckets larger than LDS (many repeats of few keys) are sorted in global memory by their
+// workgroup with a stable LSD radix sort.
+constexpr int kBucketCap = kTile;        // composites a bucket may sort in LDS (2048)
+constexpr int kBkTile = kTile;           // keys per workgroup of the histogram and the scatter
+constexpr uint32_t kBkMaxBuckets = 8192; // LDS counters per workgroup
+
+// Bucket of a key; keys outside [0, key_bound) (outside the contract) land in the last bucket
+// instead of outside the arrays.
+__device__ __forceinline__ uint32_t bucket_of(uint64_t key, int shift, uint32_t nb) {
+    const uint64_t b = key >> shift;
+    return b < nb ? static_cast<uint32_t>(b) : nb - 1;
+}
+
+__device__ __forceinline__ uint64_t composite(uint64_t key, uint64_t base, uint32_t pos) {
+    return ((key - base) << 32) | pos;
+}
+
+// Tile t's bucket counts into mat[t * nb + b] (coalesced rows).
+__global__ __launch_bounds__(kThreads) void bk_hist(const uint64_t *keys, int64_t n, int shift,
+                                                    uint32_t nb, uint32_t *mat) {
+    __shared__ uint32_t s_h[kBkMaxBuckets];
+    const int tid = threadIdx.x;
+    for (uint32_t b = tid; b < nb; b += kThreads) s_h[b] = 0u;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBkTile;
+    uint64_t k[kItems];
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+        const int64_t i = base + e * kThreads + tid;
+        k[e] = i < n ? keys[i] : ~0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kItems; ++e)
+        if (base + e * kThreads + tid < n) atomicAdd(&s_h[bucket_of(k[e], shift, nb)], 1u);
+    __syncthreads();
+    uint32_t *row = mat + static_cast<uint64_t>(blockIdx.x) * nb;
+    for (uint32_t b = tid; b < nb; b += kThreads) row[b] = s_h[b];
+}
+
+// One thread per bucket: its column of tile counts becomes the exclusive prefix over the tiles
+// (in place), its total is scanned within the block (excl[b]) and the block's sum goes to btot.
+__global__ __launch_bounds__(kThreads) void bk_prefix(uint32_t *mat, uint32_t nb, uint32_t ntiles,
+                                                      uint32_t *excl, uint32_t *btot) {
+    __shared__ uint32_t s_wtot[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t b = blockIdx.x * kThreads + tid;
+    uint32_t tot = 0;
+    if (b < nb) {
+        uint32_t t = 0;
+        for (; t + 32 <= ntiles; t += 32) {
+            uint32_t c[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) c[u] = mat[static_cast<uint64_t>(t + u) * nb + b];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                mat[static_cast<uint64_t>(t + u) * nb + b] = tot;
+                tot += c[u];
+            }
+        }
+        for (; t < ntiles; ++t) {
+            const uint32_t c = mat[static_cast<uint64_t>(t) * nb + b];
+            mat[static_cast<uint64_t>(t) * nb + b] = tot;
+            tot += c;
+        }
+    }
+    const uint32_t incl = wave_inclusive_scan(tot, lane);
+    if (lane == 63) s_wtot[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (int w = 0; w < kThreads / 64; ++w) {
+        if (w < wave) before += s_wtot[w];
+        all += s_wtot[w];
+    }
+    if (b < nb) excl[b] = before + incl - tot;
+    if (tid == 0) btot[blockIdx.x] = all;
+}
+
+// Exclusive prefix of the (<= 32) block sums of bk_prefix, into s_bp, by wave 0.
+__device__ __forceinline__ void block_prefix(const uint32_t *btot, uint32_t nb, uint32_t *s_bp, int tid) {
+    const uint32_t nblk = (nb + kThreads - 1) / kThreads;
+    if (tid < 64) {
+        const uint32_t v = static_cast<uint32_t>(tid) < nblk ? btot[tid] : 0u;
+        const uint32_t incl = wave_inclusive_scan(v, tid);
+        if (static_cast<uint32_t>(tid) < nblk) s_bp[tid] = incl - v;
+    }
+}
+
+// Each tile's keys into their buckets: slot = bucket start + the bucket's keys in earlier tiles
+// + an LDS counter (the order inside a bucket is arbitrary: bk_sort orders by position). The
+// blocks also write the bucket starts (start[nb] = n).
+__global__ __launch_bounds__(kThreads) void bk_scatter(const uint64_t *keys, int64_t n, int shift,
+                                                       uint32_t nb, const uint32_t *mat,
+                                                       const uint32_t *excl, const uint32_t *btot,
+                                                       uint64_t *bkeys, uint32_t *bpos,
+                                                       uint32_t *start) {
+    __shared__ uint32_t s_base[kBkMaxBuckets];
+    __shared__ uint32_t s_bp[kBkMaxBuckets / kThreads];
+    const int tid = threadIdx.x;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBkTile;
+    uint64_t k[kItems];
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+        const int64_t i = base + e * kThreads + tid;
+        k[e] = i < n ? keys[i] : 0ull;
+    }
+    block_prefix(btot, nb, s_bp, tid);
+    __syncthreads();
+    const uint32_t *row = mat + static_cast<uint64_t>(blockIdx.x) * nb;
+    for (uint32_t b = tid; b < nb; b += kThreads) s_base[b] = s_bp[b / kThreads] + excl[b] + row[b];
+    for (uint32_t b = blockIdx.x * kThreads + tid; b < nb; b += gridDim.x * kThreads)
+        start[b] = s_bp[b / kThreads] + excl[b];
+    if (blockIdx.x == 0 && tid == 0) start[nb] = static_cast<uint32_t>(n);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) {
+        const int64_t i = base + e * kThreads + tid;
+        if (i < n) {
+            const uint32_t slot = atomicAdd(&s_base[bucket_of(k[e], shift, nb)], 1u);
+            bkeys[slot] = k[e];
+            bpos[slot] = static_cast<uint32_t>(i);
+        }
+    }
+}
+
+// Stable LSD radix sort of the n composites at a (ping-ponging with t, 8-bit digits, `bits`
+// significant bits) by one workgroup; the result ends in a.
+__device__ void wg_radix_sort(uint64_t *a, uint64_t *t, uint32_t n, int bits) {
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ uint32_t s_wcnt[kThreads / 64][kBins];
+    __shared__ uint32_t s_wtot[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int passes = (bits + 7) / 8;
+    uint64_t *src = a, *dst = t;
+    for (int pass = 0; pass < passes; ++pass) {
+        const int sh = 8 * pass;
+        s_hist[tid] = 0u;
+        __syncthreads();
+        for (uint32_t i = tid; i < n; i += kThreads) atomicAdd(&s_hist[(src[i] >> sh) & (kBins - 1)], 1u);
+        __syncthreads();
+        {   // exclusive scan of the 256 digit counts, thread d holds digit d
+            const uint32_t c = s_hist[tid];
+            const uint32_t incl = wave_inclusive_scan(c, lane);
+            if (lane == 63) s_wtot[wave] = incl;
+            __syncthreads();
+            uint32_t before = 0;
+            for (int w = 0; w < wave; ++w) before += s_wtot[w];
+            s_hist[tid] = before + incl - c;  // the digit's next output slot
+        }
+        __syncthreads();
+        for (uint32_t i0 = 0; i0 < n; i0 += kThreads) {
+            const uint32_t i = i0 + tid;
+            const bool valid = i < n;
+            const uint64_t v = valid ? src[i] : 0ull;
+            const int digit = static_cast<int>((v >> sh) & (kBins - 1));
+#pragma unroll
+            for (int u = 0; u < kBins / 64; ++u) s_wcnt[wave][lane * (kBins / 64) + u] = 0u;
+            uint64_t same = __ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 8; ++bit) {
+                const bool set = (digit >> bit) & 1;
+                const uint64_t bb = __ballot(set);
+                same &= set ? bb : ~bb;
+            }
+            const int rank = __popcll(same & lanes_below(lane));
+            __syncthreads();
+            if (valid && rank == 0) s_wcnt[wave][digit] = static_cast<uint32_t>(__popcll(same));
+            __syncthreads();
+            if (valid) {
+                uint32_t off = s_hist[digit] + static_cast<uint32_t>(rank);
+                for (int w = 0; w < wave; ++w) off += s_wcnt[w][digit];
+                dst[off] = v;
+            }
+            __syncthreads();
+            uint32_t add = 0;
+#pragma unroll
+            for (int w = 0; w < kThreads / 64; ++w) add += s_wcnt[w][tid];
+            s_hist[tid] += add;
+            __syncthreads();
+        }
+        uint64_t *x = src;
+        src = dst;
+        dst = x;
+    }
+    if (src != a)
+        for (uint32_t i = tid; i < n; i += kThreads) a[i] = src[i];
+    __syncthreads();
+}
+
+// Rank sort of the n (<= ITEMS * 256) distinct composites in s_c into out: each composite's
+// rank is how many are smaller (every lane reads the same s_c[j] at once, an LDS broadcast);
+// returns how many of this thread's composites are the first of their key.
+template <int ITEMS>
+__device__ __forceinline__ uint32_t rank_sort(const uint64_t *s_c, uint32_t n, uint64_t *out, int tid) {
+    uint64_t mine[ITEMS];
+    uint32_t rank[ITEMS], same_before[ITEMS];
+#pragma unroll
+    for (int e = 0; e < ITEMS; ++e) {
+        const uint32_t i = tid + e * kThreads;
+        mine[e] = i < n ? s_c[i] : ~0ull;
+        rank[e] = 0u;
+        same_before[e] = 0u;
+    }
+    uint32_t j = 0;
+    for (; j + 4 <= n; j += 4) {
+        uint64_t c[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) c[u] = s_c[j + u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < ITEMS; ++e) {
+                const bool less = c[u] < mine[e];
+                rank[e] += less ? 1u : 0u;
+                same_before[e] += (less && (c[u] >> 32) == (mine[e] >> 32)) ? 1u : 0u;
+            }
+    }
+    for (; j < n; ++j) {
+        const uint64_t c = s_c[j];
+#pragma unroll
+        for (int e = 0; e < ITEMS; ++e) {
+            const bool less = c < mine[e];
+            rank[e] += less ? 1u : 0u;
+            same_before[e] += (less && (c >> 32) == (mine[e] >> 32)) ? 1u : 0u;
+        }
+    }
+    uint32_t heads = 0;
+#pragma unroll
+    for (int e = 0; e < ITEMS; ++e)
+        if (tid + e * kThreads < n) {
+            out[rank[e]] = mine[e];
+            heads += same_before[e] == 0u ? 1u : 0u;  // the first of its key
+        }
+    return heads;
+}
+
+// One workgroup per bucket: the bucket's composites sorted into comp[lo, hi) -- a rank sort in
+// LDS (each composite's rank = how many are smaller; every lane reads the same s_c[j] at once,
+// an LDS broadcast), or the global radix sort above for buckets larger than LDS -- and the
+// number of unique keys in it into ucount[b].
+__global__ __launch_bounds__(kThreads) void bk_sort(const uint64_t *bkeys, const uint32_t *bpos,
+                                                    const uint32_t *start, int shift, uint64_t *comp,
+                                                    uint64_t *tmp, uint32_t *ucount) {
+    __shared__ uint64_t s_c[kBucketCap];
+    __shared__ uint32_t s_red[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t b = blockIdx.x;
+    const uint32_t lo = start[b], n = start[b + 1] - lo;
+    const uint64_t base = static_cast<uint64_t>(b) << shift;
+    uint32_t heads = 0;
+    if (n <= static_cast<uint32_t>(kBucketCap)) {
+        for (uint32_t i = tid; i < n; i += kThreads) s_c[i] = composite(bkeys[lo + i], base, bpos[lo + i]);
+        __syncthreads();
+        // as many items per thread as the bucket needs (a uniform branch)
+        if (n <= kThreads)
+            heads = rank_sort<1>(s_c, n, comp + lo, tid);
+        else if (n <= 2 * kThreads)
+            heads = rank_sort<2>(s_c, n, comp + lo, tid);
+        else if (n <= 4 * kThreads)
+            heads = rank_sort<4>(s_c, n, comp + lo, tid);
+        else
+            heads = rank_sort<kItems>(s_c, n, comp + lo, tid);
+    } else {
+        uint64_t *a = comp + lo;
+        for (uint32_t i = tid; i < n; i += kThreads) a[i] = composite(bkeys[lo + i], base, bpos[lo + i]);
+        __syncthreads();
+        wg_radix_sort(a, tmp + lo, n, 32 + shift);
+        for (uint32_t i = tid; i < n; i += kThreads) heads += (i == 0 || (a[i] >> 32) != (a[i - 1] >> 32)) ? 1u : 0u;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) heads += __shfl_xor(heads, off, 64);
+    if (lane == 0) s_red[wave] = heads;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t t = 0;
+        for (int w = 0; w < kThreads / 64; ++w) t += s_red[w];
+        ucount[b] = t;
+    }
+}
+
+// The fp32 sum of rows pos(a), pos(a+1), ... pos(e-1), columns [c0, c0 + kCols), added in that
+// order from +0.0 (the rounding of CPU index_add_), into out.
+template <typename G, int kCols, typename PosAt>
+__device__ __forceinline__ void sum_segment(const G *grads, uint32_t dim, uint32_t c0, uint32_t a,
+                                            uint32_t e, PosAt pos_at, float *out) {
+    float acc[kCols], x[kCols];
+    load_cols(grads + static_cast<uint64_t>(pos_at(a)) * dim + c0, x);
+#pragma unroll
+    for (int c = 0; c < kCols; ++c) acc[c] = 0.f + x[c];
+    uint32_t i = a + 1;
+    for (; i + 4 <= e; i += 4) {
+        float y[4][kCols];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_cols(grads + static_cast<uint64_t>(pos_at(i + u)) * dim + c0, y[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + y[u][c];
+    }
+    for (; i < e; ++i) {
+        load_cols(grads + static_cast<uint64_t>(pos_at(i)) * dim + c0, x);
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + x[c];
+    }
+    if constexpr (kCols == 4)
+        *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    else
+        out[0] = acc[0];
+}
+
+// One workgroup per bucket: its unique keys are numbered after those of the buckets before it
+// (a block sum over ucount[0, b)); it writes uniq, inv and, with gradients, each unique key's
+// fp32 sum of its gradient rows in increasing position order (bit-exact with CPU index_add_).
+// The bucket's positions and segment starts are staged in LDS, and the workgroup sums every
+// (segment, run of kCols columns) with all its threads; a bucket larger than LDS (rare: many
+// repeats of few keys) has each segment summed by the thread of its first element. The last
+// bucket writes the count.
+template <typename G, int kCols>
+__global__ __launch_bounds__(kThreads) void bk_emit(const uint64_t *comp, const uint32_t *start,
+                                                    const uint32_t *ucount, uint32_t nb, int shift,
+                                                    const G *grads, uint32_t dim, int64_t *uniq,
+                                                    int64_t *inv, float *gsum, int64_t *count) {
+    __shared__ uint32_t s_scan[kThreads];
+    __shared__ uint32_t s_red[kThreads / 64];
+    __shared__ uint32_t s_pos[kBucketCap];
+    __shared__ uint32_t s_seg[kBucketCap + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t b = blockIdx.x;
+    const uint32_t lo = start[b], n = start[b + 1] - lo;
+    const uint64_t base = static_cast<uint64_t>(b) << shift;
+    const uint64_t *sorted = comp + lo;
+    const bool in_lds = n <= static_cast<uint32_t>(kBucketCap);
+    // unique keys of the earlier buckets: 16-byte loads, all of a thread's issued together
+    uint32_t before = 0;
+    {
+        const uint4 *u4 = reinterpret_cast<const uint4 *>(ucount);
+        const uint32_t words = (b + 3) / 4;  // ucount is padded to a multiple of 4 entries
+        for (uint32_t w0 = tid; w0 < words; w0 += 4 * kThreads) {
+            uint4 x[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t w = w0 + q * kThreads;
+                x[q] = w < words ? u4[w] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t j = 4 * (w0 + q * kThreads);
+                before += (j + 0 < b ? x[q].x : 0u) + (j + 1 < b ? x[q].y : 0u) +
+                          (j + 2 < b ? x[q].z : 0u) + (j + 3 < b ? x[q].w : 0u);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) before += __shfl_xor(before, off, 64);
+    if (lane == 0) s_red[wave] = before;
+    __syncthreads();
+    uint32_t run = 0;  // unique keys numbered before this tile
+    for (int w = 0; w < kThreads / 64; ++w) run += s_red[w];
+    const uint32_t first_u = run;
+    if (b == nb - 1 && tid == 0) *count = static_cast<int64_t>(run) + ucount[b];
+    const uint32_t runs = dim / kCols;
+    for (uint32_t t0 = 0; t0 < n; t0 += kThreads * kItems) {
+        const uint32_t i0 = t0 + static_cast<uint32_t>(tid) * kItems;
+        uint64_t v[kItems];
+        uint32_t c = 0;
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) v[e] = i0 + e < n ? sorted[i0 + e] : 0ull;
+        const uint64_t prev = i0 > 0 && i0 < n ? sorted[i0 - 1] : ~0ull;
+        bool head[kItems];
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) {
+            const uint64_t p = e == 0 ? prev : v[e - 1];
+            head[e] = i0 + e < n && (i0 + e == 0 || (v[e] >> 32) != (p >> 32));
+            c += head[e] ? 1u : 0u;
+        }
+        s_scan[tid] = c;
+        __syncthreads();
+        for (int off = 1; off < kThreads; off <<= 1) {
+            const uint32_t x = tid >= off ? s_scan[tid - off] : 0u;
+            __syncthreads();
+            s_scan[tid] += x;
+            __syncthreads();
+        }
+        uint32_t u = run + s_scan[tid] - c;  // unique keys before this thread's first element
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) {
+            const uint32_t i = i0 + e;
+            if (i < n) {
+                const uint32_t pos = static_cast<uint32_t>(v[e]);
+                if (head[e]) {
+                    uniq[u] = static_cast<int64_t>(base + (v[e] >> 32));
+                    if (in_lds) {
+                        s_seg[u - first_u] = i;
+                    } else if (grads != nullptr) {
+                        uint32_t end = i + 1;
+                        while (end < n && (sorted[end] >> 32) == (v[e] >> 32)) ++end;
+                        for (uint32_t r = 0; r < runs; ++r)
+                            sum_segment<G, kCols>(grads, dim, r * kCols, i, end,
+                                                  [&](uint32_t k) { return static_cast<uint32_t>(sorted[k]); },
+                                                  gsum + static_cast<uint64_t>(u) * dim + r * kCols);
+                    }
+                    ++u;
+                }
+                inv[pos] = static_cast<int64_t>(u) - 1;
+                if (in_lds) s_pos[i] = pos;
+            }
+        }
+        run += s_scan[kThreads - 1];
+        __syncthreads();
+    }
+    if (grads == nullptr || !in_lds) return;
+    const uint32_t nseg = run - first_u;
+    if (tid == 0) s_seg[nseg] = n;
+    __syncthreads();
+    for (uint32_t it = tid; it < nseg * runs; it += kThreads) {
+        const uint32_t j = it / runs, c0 = (it - j * runs) * kCols;
+        sum_segment<G, kCols>(grads, dim, c0, s_seg[j], s_seg[j + 1], [&](uint32_t k) { return s_pos[k]; },
+                              gsum + static_cast<uint64_t>(first_u + j) * dim + c0);
+    }
 }
 
 // ---- squared norm ---------------------------------------------------------------------------
@@ -615,12 +1046,24 @@ int sort_bits(int64_t key_bound) {
 
 struct DedupLayout {
     int nblocks, hist_stride;
-    size_t keys_b, pos_a, pos_b, hist, heads, seg_start, seg_pos, total;
+    uint32_t nb_max;  // buckets the bucket dedup may use (0: it is not used for this n)
+    uint32_t ntiles;  // its histogram tiles
+    size_t keys_b, pos_a, pos_b, hist, heads, seg_start, seg_pos, tmp, bk_mat, bk_excl, bk_btot,
+        bk_start, bk_ucount, total;
 };
+
+// The bucket dedup aims at kBucketMean keys per bucket (one LDS sort each) and is used up to
+// kBucketMaxN keys (beyond, buckets would average more than 256 keys: the radix sort then).
+constexpr int64_t kBucketMean = 24;
+constexpr int64_t kBucketMaxN = int64_t{1} << 21;
 
 DedupLayout dedup_layout(int64_t n) {
     DedupLayout l{};
     l.nblocks = static_cast<int>(ceil_div(n, kTile));
+    if (n <= kBucketMaxN) {
+        l.nb_max = static_cast<uint32_t>(std::min<int64_t>(n / kBucketMean + 1, kBkMaxBuckets));
+        l.ntiles = static_cast<uint32_t>(ceil_div(n, kBkTile));
+    }
     auto up = [](size_t x) { return (x + 255) & ~size_t{255}; };
     size_t off = 0;
     l.keys_b = off; off += up(static_cast<size_t>(n) * 8 * 2);  // two key buffers
@@ -631,8 +1074,27 @@ DedupLayout dedup_layout(int64_t n) {
     l.heads = off; off += up(static_cast<size_t>(l.nblocks + 1) * 4);
     l.seg_start = off; off += up(static_cast<size_t>(n + 1) * 4);
     l.seg_pos = off; off += up(static_cast<size_t>(n) * 4);
+    if (l.nb_max > 0) {
+        l.tmp = off; off += up(static_cast<size_t>(n) * 8);
+        l.bk_mat = off; off += up(static_cast<size_t>(l.nb_max) * l.ntiles * 4);
+        l.bk_excl = off; off += up(static_cast<size_t>(l.nb_max) * 4);
+        l.bk_btot = off; off += up(static_cast<size_t>(kBkMaxBuckets / kThreads) * 4);
+        l.bk_start = off; off += up(static_cast<size_t>(l.nb_max + 1) * 4);
+        l.bk_ucount = off; off += up(static_cast<size_t>(l.nb_max + 3) / 4 * 16);  // 16-byte reads
+    }
     l.total = off;
     return l;
+}
+
+// Bucket shift for the bucket dedup: the smallest s whose buckets (key >> s) number at most
+// nb_max; -1 when the bucket dedup is not used (nb_max 0) or the low key bits below a bucket
+// would not fit the 32 bits of a composite.
+int bucket_shift(int64_t key_bound, uint32_t nb_max) {
+    if (nb_max == 0) return -1;
+    const uint64_t top = static_cast<uint64_t>(key_bound - 1);
+    int s = 0;
+    while (s < 63 && (top >> s) + 1 > nb_max) ++s;
+    return s <= 32 ? s : -1;
 }
 
 }  // namespace
@@ -678,27 +1140,73 @@ extern "C" int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const
     uint32_t *seg_start = reinterpret_cast<uint32_t *>(ws + l.seg_start);
     uint32_t *seg_pos = reinterpret_cast<uint32_t *>(ws + l.seg_pos);
 
-    const int passes = (sort_bits(key_bound) + 7) / 8;
-    const uint64_t *kin = reinterpret_cast<const uint64_t *>(keys);
-    const uint32_t *pin = nullptr;
     const dim3 grid(static_cast<unsigned>(l.nblocks)), block(kThreads);
-    int cur = 0;
-    for (int p = 0; p < passes; ++p) {
-        const int shift = 8 * p;
-        hipLaunchKernelGGL(rs_hist, grid, block, 0, s, kin, n, shift, hist, l.nblocks, l.hist_stride);
-        hipLaunchKernelGGL(rs_scatter, grid, block, 0, s, kin, pin, kb[cur], pb[cur], n, shift, hist,
-                           l.hist_stride);
-        kin = kb[cur];
-        pin = pb[cur];
-        cur ^= 1;
+    const int shift = bucket_shift(key_bound, l.nb_max);
+    const uint32_t *pin = nullptr;
+    if (shift >= 0) {
+        // bucket dedup: histograms, prefix, scatter, per-bucket sort, emit
+        const uint32_t nb = static_cast<uint32_t>((static_cast<uint64_t>(key_bound - 1) >> shift) + 1);
+        uint32_t *mat = reinterpret_cast<uint32_t *>(ws + l.bk_mat);
+        uint32_t *excl = reinterpret_cast<uint32_t *>(ws + l.bk_excl);
+        uint32_t *btot = reinterpret_cast<uint32_t *>(ws + l.bk_btot);
+        uint32_t *bstart = reinterpret_cast<uint32_t *>(ws + l.bk_start);
+        uint32_t *ucount = reinterpret_cast<uint32_t *>(ws + l.bk_ucount);
+        uint64_t *bkeys = kb[0], *comp = kb[1];
+        uint64_t *tmp = reinterpret_cast<uint64_t *>(ws + l.tmp);
+        uint32_t *bpos = pb[0], *spos = pb[1];
+        const uint64_t *k64 = reinterpret_cast<const uint64_t *>(keys);
+        const dim3 tgrid(l.ntiles), pgrid(static_cast<unsigned>(ceil_div(nb, kThreads))), bgrid(nb);
+        hipLaunchKernelGGL(bk_hist, tgrid, block, 0, s, k64, n, shift, nb, mat);
+        hipLaunchKernelGGL(bk_prefix, pgrid, block, 0, s, mat, nb, l.ntiles, excl, btot);
+        hipLaunchKernelGGL(bk_scatter, tgrid, block, 0, s, k64, n, shift, nb, mat, excl, btot, bkeys,
+                           bpos, bstart);
+        hipLaunchKernelGGL(bk_sort, bgrid, block, 0, s, bkeys, bpos, bstart, shift, comp, tmp, ucount);
+        const size_t gsz = grad_dtype == ME_F32 ? 4 : 2;
+        const bool vec4 = grads != nullptr && dim % 4 == 0 &&
+                          reinterpret_cast<uintptr_t>(grads) % (4 * gsz) == 0 &&
+                          reinterpret_cast<uintptr_t>(gsum) % 16 == 0;
+        const uint32_t d = grads != nullptr ? static_cast<uint32_t>(dim) : 0u;
+        if (grads == nullptr || grad_dtype == ME_F32) {
+            const float *g = static_cast<const float *>(grads);
+            if (vec4)
+                hipLaunchKernelGGL((bk_emit<float, 4>), bgrid, block, 0, s, comp, bstart, ucount, nb, shift,
+                                   g, d, uniq, inv, gsum, count);
+            else
+                hipLaunchKernelGGL((bk_emit<float, 1>), bgrid, block, 0, s, comp, bstart, ucount, nb, shift,
+                                   g, d, uniq, inv, gsum, count);
+        } else {
+            const uint16_t *g = static_cast<const uint16_t *>(grads);
+            if (vec4)
+                hipLaunchKernelGGL((bk_emit<uint16_t, 4>), bgrid, block, 0, s, comp, bstart, ucount, nb,
+                                   shift, g, d, uniq, inv, gsum, count);
+            else
+                hipLaunchKernelGGL((bk_emit<uint16_t, 1>), bgrid, block, 0, s, comp, bstart, ucount, nb,
+                                   shift, g, d, uniq, inv, gsum, count);
+        }
+        (void)spos;
+        return check_launch("me_dedup (buckets)");
+    } else {
+        // LSD radix sort of (key, position), 8 bits per pass, then the segments
+        const int passes = (sort_bits(key_bound) + 7) / 8;
+        const uint64_t *kin = reinterpret_cast<const uint64_t *>(keys);
+        int cur = 0;
+        for (int p = 0; p < passes; ++p) {
+            const int sh = 8 * p;
+            hipLaunchKernelGGL(rs_hist, grid, block, 0, s, kin, n, sh, hist, l.nblocks, l.hist_stride);
+            hipLaunchKernelGGL(rs_scatter, grid, block, 0, s, kin, pin, kb[cur], pb[cur], n, sh, hist,
+                               l.hist_stride);
+            kin = kb[cur];
+            pin = pb[cur];
+            cur ^= 1;
+        }
+        int st = check_launch("me_dedup (sort)");
+        if (st != ME_OK) return st;
+        hipLaunchKernelGGL(seg_count, grid, block, 0, s, kin, n, heads);
+        hipLaunchKernelGGL(seg_write, grid, block, 0, s, kin, pin, n, heads, l.nblocks, uniq, inv,
+                           seg_start, seg_pos, count);
+        st = check_launch("me_dedup (segments)");
+        if (st != ME_OK || grads == nullptr) return st;
     }
-    int st = check_launch("me_dedup (sort)");
-    if (st != ME_OK) return st;
-    hipLaunchKernelGGL(seg_count, grid, block, 0, s, kin, n, heads);
-    hipLaunchKernelGGL(seg_write, grid, block, 0, s, kin, pin, n, heads, l.nblocks, uniq, inv,
-                       seg_start, seg_pos, count);
-    st = check_launch("me_dedup (segments)");
-    if (st != ME_OK || grads == nullptr) return st;
     // four columns per thread when every row start is aligned for the vector loads and stores
     const size_t gsz = grad_dtype == ME_F32 ? 4 : 2;
     const bool vec = dim % 4 == 0 && reinterpret_cast<uintptr_t>(grads) % (4 * gsz) == 0 &&

@@ -42,6 +42,33 @@ def test_dedup_bit_exact(n, bound, dim):
     _check_dedup(keys, grads, bound)
 
 
+@pytest.mark.parametrize("case", ["all_equal", "clustered", "hot_keys", "large_random", "tiny"])
+def test_dedup_bucket_paths_bit_exact(case):
+    # keys that fit a bucket composite take the bucket dedup: buckets sorted in LDS, buckets too
+    # large for LDS (repeats, or keys far denser than key_bound suggests) sorted in global
+    # memory first; every case against the oracle's unique / inverse / ordered fp32 sums
+    g = torch.Generator().manual_seed(7)
+    if case == "all_equal":
+        n, bound = 5000, 1000
+        keys = torch.full((n,), 417, dtype=torch.long)
+    elif case == "clustered":
+        n, bound = 10000, 10**9
+        keys = torch.randint(0, 3000, (n,), generator=g)
+    elif case == "hot_keys":
+        n, bound = 60000, 1 << 24
+        keys = torch.randint(0, bound, (n,), generator=g)
+        hot = torch.randint(0, bound, (5,), generator=g)
+        keys[torch.randperm(n, generator=g)[:20000]] = hot[torch.randint(0, 5, (20000,), generator=g)]
+    elif case == "large_random":
+        n, bound = 300000, 79_691_776
+        keys = torch.randint(0, bound, (n,), generator=g)
+    else:
+        n, bound = 3, 2
+        keys = torch.tensor([1, 0, 1])
+    grads = torch.randn(n, 16, generator=g) * torch.logspace(-3, 3, n).unsqueeze(1)
+    _check_dedup(keys, grads, bound)
+
+
 def test_dedup_bf16_grads_and_keys_only():
     g = torch.Generator().manual_seed(1)
     keys = torch.randint(0, 300, (4000,), generator=g)
