@@ -10,13 +10,16 @@
 //   adam       micro_engram/optim.py:65-133, the sparse-gradient branch (88-97), per-row second
 //              moment (112-114) and write-back with stochastic_bf16 (33-44, 120-132)
 //
-// Dedup = a stable LSD radix sort of (key, position) pairs, 8 key bits per pass: per-block digit
-// histograms, one scan over [digit][block], then a scatter that ranks equal digits inside each
-// wave with 8 ballots (lower lane = earlier element), so every pass keeps the positions of equal
-// keys in increasing order. Segment heads of the sorted keys then give the unique keys, the
-// inverse, and per-segment ranges; one thread per (segment, 4 columns) sums the gradient rows of
-// its segment in ascending position order starting from +0.0 -- the order, and so the rounding,
-// of CPU index_add_.
+// Dedup, two paths with the same results. Keys whose bits below a bucket fit 32 (the usual case:
+// table offset + row): a bucket pass on the high key bits, one LDS rank sort per bucket of
+// (low key bits, position) composites, and one workgroup per bucket that numbers its unique keys
+// after the earlier buckets', writes the unique keys and the inverse, and sums each segment's
+// gradient rows (bk_* kernels below). Wider keys: a stable LSD radix sort of (key, position)
+// pairs, 8 key bits per pass (per-block digit histograms, then a scatter that ranks equal
+// digits inside each wave with 8 ballots, lower lane = earlier element), segment heads, and
+// one thread per (segment, 4 columns) for the sums. Either way a segment's gradient rows are
+// summed in ascending position order starting from +0.0 -- the order, and so the rounding, of
+// CPU index_add_.
 #include "me_common.h"
 
 #include <algorithm>
