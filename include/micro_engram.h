@@ -168,6 +168,29 @@ int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n, int64_t mo
                      void *stream);
 
 /*
+ * me_gate_rows -- the gate and residual add of me_gate_residual from key and value projections
+ * computed elsewhere (few-token batches, where one GEMM of the memory vectors against the
+ * stacked [W_K; W_V] on the library BLAS fills the part and me_gate_residual's 256 x 256 tiles
+ * would not). Replaces the rest of MicroEngram.inject after the two nn.Linear calls
+ * (micro_engram/module.py:240-261), with the same arithmetic as me_gate_residual:
+ *
+ *   h = rms_norm(hidden) [* (1 + q_scale_delta)], k = rms_norm(K) [* (1 + k_scale_delta)]
+ *   s = sum(h k) / sqrt(model_dim); ME_GATE_SCALAR_SQRT: s = sign(s) sqrt(max(|s|, 1e-6))
+ *   out = hidden + round_hidden(sigmoid(s) * V * keep)
+ *
+ *   hidden, out   [n, model_dim] of hidden_dtype (out may equal hidden)
+ *   k_proj, v_proj  rows of K and V (dtype), kv_stride elements apart (e.g. the two halves of
+ *                 one [n, 2 model_dim] GEMM output); model_dim and kv_stride multiples of 8, every
+ *                 tensor 16-byte aligned
+ *   q/k_scale_delta, keep, alpha_out, row_stats   as for me_gate_residual
+ */
+int me_gate_rows(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                 const void *k_proj, const void *v_proj, int64_t kv_stride, int dtype,
+                 const void *q_scale_delta, const void *k_scale_delta, int scale_dtype,
+                 int gate_mode, const uint8_t *keep, void *out, float *alpha_out,
+                 float *row_stats, void *stream);
+
+/*
  * me_gate_backward_workspace_size -- bytes of workspace me_gate_backward needs.
  */
 int me_gate_backward_workspace_size(int64_t n, int64_t model_dim, size_t *bytes);

@@ -317,6 +317,47 @@ def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep
     return res
 
 
+@torch.library.custom_op("micro_engram_amd::gate_residual_rows", mutates_args=())
+def gate_residual_rows(hidden: torch.Tensor, mem: torch.Tensor, w_kv: torch.Tensor,
+                       q_scale_delta: Optional[torch.Tensor], k_scale_delta: Optional[torch.Tensor],
+                       gate_mode: int, keep: Optional[torch.Tensor], with_alpha: bool,
+                       with_stats: bool = False) -> List[torch.Tensor]:
+    """gate_residual for few tokens: [K | V] = mem @ w_kv^T as one GEMM on the library BLAS
+    (w_kv = [W_K; W_V], [2d, M]; K and V rounded to mem's dtype, as the two nn.Linear calls of
+    module.py:245, 254 give them), then the gate and residual add in me_gate_rows."""
+    dev = require_gpu(hidden, mem, w_kv, q_scale_delta, k_scale_delta, keep)
+    d = hidden.shape[-1]
+    if w_kv.dim() != 2 or w_kv.shape[0] != 2 * d:
+        raise ValueError(f"[micro_engram] stacked weight {tuple(w_kv.shape)} is not [2 * {d}, M]")
+    x, mem, _wk, _wv, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M = \
+        _gate_operands(hidden, mem, w_kv[:d], w_kv[d:], q_scale_delta, k_scale_delta, gate_mode, keep)
+    kv = torch.mm(mem, w_kv.t())
+    out = torch.empty_like(x)
+    alpha = torch.empty(N, dtype=torch.float32, device=dev) if with_alpha else None
+    stats = torch.empty((N, 4), dtype=torch.float32, device=dev) if with_stats else None
+    call("me_gate_rows", x.data_ptr(), dtype_code(x), N, d, kv.data_ptr(),
+         kv.data_ptr() + d * kv.element_size(), 2 * d, dtype_code(kv), _p(q_scale_delta),
+         _p(k_scale_delta), scale_code, gate_mode, _p(keep_u8), out.data_ptr(), _p(alpha),
+         _p(stats), stream_of(dev))
+    res = [out.reshape(hidden.shape)]
+    if with_alpha:
+        res.append(alpha)
+    if with_stats:
+        res.append(stats)
+    return res
+
+
+@gate_residual_rows.register_fake
+def _(hidden, mem, w_kv, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha, with_stats=False):
+    n = hidden.numel() // hidden.shape[-1]
+    res = [torch.empty_like(hidden)]
+    if with_alpha:
+        res.append(hidden.new_empty((n,), dtype=torch.float32))
+    if with_stats:
+        res.append(hidden.new_empty((n, 4), dtype=torch.float32))
+    return res
+
+
 def gate_backward_workspace_bytes(n, d):
     size = ctypes.c_size_t(0)
     call("me_gate_backward_workspace_size", n, d, ctypes.byref(size))

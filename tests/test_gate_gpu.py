@@ -19,6 +19,14 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.fixture(autouse=True, params=["fused", "rows"])
+def gate_path(request, monkeypatch):
+    """Every test of this file runs on both gate paths of MicroEngram: the fused two-pass kernel
+    (me_gate_residual) and, for few tokens, the library GEMM + row kernel (me_gate_rows)."""
+    monkeypatch.setattr(MicroEngram, "few_tokens_max", 0 if request.param == "fused" else 1 << 30)
+    return request.param
+
+
 def _bf16_ulp(x):
     x = x.abs().float().clamp_min(2.0 ** -126)
     return torch.pow(2.0, torch.floor(torch.log2(x)) - 7)
@@ -143,6 +151,7 @@ def test_grad_path_forward_equals_fused(dtype):
     # with gradients the forward hashes, gathers through the differentiable row lookup and
     # keeps the gate's row sums; its output is the fused inference forward's, bit for bit
     eng = _make(dtype, d=64, dim=8, heads=2, orders=(2, 3, 4)).train()
+    eng.few_tokens_max = 0  # the fused kernel, which the gradient path also runs
     ids = torch.randint(0, 1000, (2, 70), device=DEV)
     hidden = torch.randn(2, 70, 64).to(dtype).to(DEV)
     with torch.no_grad():
@@ -224,3 +233,52 @@ def test_projection_rounds_to_nearest_even():
     assert torch.equal(alpha.cpu(), torch.full((4,), 0.5))
     want = (wv[:, 0].float() + t.float()).to(torch.bfloat16)  # fp32 sum is exact; RNE to bf16
     assert torch.equal((out.cpu().float() * 2).to(torch.bfloat16), want.expand(4, d))
+
+
+@pytest.mark.parametrize("hdt,tdt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                     (torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("gate", [0, 1])
+@pytest.mark.parametrize("n,d,m", [(1, 64, 32), (37, 520, 96), (256, 1024, 256), (300, 5376, 1536)])
+def test_rows_path_matches_fused_and_oracle(hdt, tdt, gate, n, d, m):
+    # the few-token path (one GEMM against [W_K; W_V], then me_gate_rows) against the oracle and
+    # the fused kernel on the same operands, with a keep mask and the row stats of the backward
+    g = torch.Generator().manual_seed(n * 7 + d)
+    hidden = (torch.randn(n, d, generator=g) * 3).to(hdt)
+    mem = (torch.randn(n, m, generator=g) * 0.5).to(tdt)
+    wk = (torch.randn(d, m, generator=g) * 0.05).to(tdt)
+    wv = (torch.randn(d, m, generator=g) * 0.05).to(tdt)
+    dq = (torch.randn(d, generator=g) * 0.1).to(tdt) if gate == 1 else None
+    dk = (torch.randn(d, generator=g) * 0.1).to(tdt) if gate == 1 else None
+    keep = torch.rand(n, generator=g) > 0.2
+    dev = [t.to(DEV) if t is not None else None for t in (hidden, mem, wk, wv, dq, dk, keep)]
+    with torch.no_grad():
+        rows = ops.gate_residual_rows(dev[0], dev[1], torch.cat([dev[2], dev[3]]), dev[4], dev[5], gate,
+                                      dev[6], True, True)
+        fused = ops.gate_residual(*dev[:6], gate, dev[6], True, True)
+    ref, alpha_ref = oracle.inject(hidden.float() if hdt == torch.float32 else hidden, mem, wk, wv,
+                                   ["scalar", "scalar_sqrt"][gate], dq, dk, keep=keep, return_alpha=True)
+    assert_close_out(rows[0], ref, hidden, hdt if tdt == hdt else torch.bfloat16)
+    tol = 1e-5 if (hdt, tdt) == (torch.float32, torch.float32) else 2e-3
+    assert (rows[1].cpu() - alpha_ref.float()).abs().max() <= tol
+    assert (rows[1] - fused[1]).abs().max() <= tol
+    # row stats: sum x^2 exact up to summation order, the gate as returned
+    assert torch.allclose(rows[2][:, 0], fused[2][:, 0], rtol=1e-5)
+    assert torch.equal(rows[2][:, 3], rows[1])
+    assert torch.equal(rows[0][~dev[6]], dev[0][~dev[6]])  # keep = False: unchanged
+
+
+def test_serving_decode_step_sampled():
+    # the serving decode workload: 256 sequences x 1 token (0-3 history tokens, -1 = none) on the
+    # Gemma-scale tables, hash_prev + inject as the vLLM layer calls them, against the oracle
+    eng = synthetic.build_engram("gemma", DEV, seed=0).eval()
+    ids, hidden = synthetic.decode_inputs(seed=2)
+    with torch.no_grad():
+        idx = eng.hash_prev(ids.to(DEV))
+        out = eng.inject(hidden.to(DEV), idx)
+    idx = torch.stack(idx)
+    mem = torch.cat([t.weight[idx[k]] for k, t in enumerate(eng.tables)], dim=-1).cpu()
+    ref = oracle.inject(hidden, mem, eng.key.weight.detach().cpu(), eng.value.weight.detach().cpu(),
+                        "scalar_sqrt", eng.q_scale.detach().cpu(), eng.k_scale.detach().cpu())
+    assert_close_out(out, ref, hidden, torch.bfloat16)
+    del eng
+    torch.cuda.empty_cache()
