@@ -20,6 +20,8 @@ all inputs already in HBM. Prints one JSON line:
                 HBM byte counters
   roofline_gate the K/V projection + gate + residual kernels: 4 * M * d FLOP per token / their
                 mean duration (graph replay, as above), against 2.5 PFLOP/s dense bf16
+  serving_decode  a decode step of 256 one-token sequences on the same engram (hash_prev +
+                inject, the calls of the vLLM decoder layer), graph replay over 16 distinct steps
   roofline_update  the training-side sparse update of a batch of this shape (dedup of the
                 196,608 lookups + row-wise Adam with stochastic rounding on the touched rows),
                 algorithmic bytes / duration (graph replay) over 16 distinct batches
@@ -232,6 +234,21 @@ def main():
         gather_ms = replay_ms([(lambda k=k: gather(k)) for k in range(CYCLE)], 2)
         gate_ms = replay_ms([(lambda k=k: gate(k)) for k in range(CYCLE)], 2)
 
+        # Serving decode on the same engram: 256 sequences x 1 token with 0-3 history tokens,
+        # hash_prev + inject as the vLLM decoder layer calls them, over 16 distinct steps
+        dsteps = []
+        for s in range(CYCLE):
+            dids, dhidden = synthetic.decode_inputs(seed=s)
+            dsteps.append((dids.to(dev), dhidden.to(dev)))
+
+        def decode(k):
+            dids, dhidden = dsteps[k % CYCLE]
+            eng.inject(dhidden, eng.hash_prev(dids))
+
+        decode_ms = replay_ms([(lambda k=k: decode(k)) for k in range(CYCLE)], 2)
+        decode_tokens = dsteps[0][0].shape[0]
+        del dsteps
+
         # The sparse update (dedup + row-wise Adam with stochastic rounding) of the same
         # batch shape, over the same cycle of distinct batches; it writes the tables, so it
         # runs after the forward measurements.
@@ -331,6 +348,12 @@ def main():
             "dedup_gbs": dedup_b / (dedup_ms * 1e-3) / 1e9,
             "adam_ms": adam_ms,
             "adam_gbs": adam_b / (adam_ms * 1e-3) / 1e9,
+        },
+        "serving_decode": {
+            "workload": "the same engram, 256 sequences x 1 token (0-3 history tokens, [256, 4] "
+                        "int32 ids with -1), hidden 5376 bf16: hash_prev + inject per step",
+            "step_us": decode_ms * 1e3,
+            "tokens_per_s": decode_tokens / (decode_ms * 1e-3),
         },
         "timing": "value: wall clock around one replay of a HIP graph of the K steps; kernel "
                   "durations: per-kernel graph replays over the 16 batches between HIP events",
