@@ -335,7 +335,7 @@ def main():
             "mean_ms": gate_ms,
         },
         "roofline_update": {
-            "kernel": "sparse update: dedup (radix sort + segment sums) + row-wise Adam with "
+            "kernel": "sparse update: dedup (bucket sort + segment sums) + row-wise Adam with "
                       "stochastic rounding",
             "bound": "hbm",
             "achieved": update_gbs,

@@ -759,9 +759,10 @@ __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
     constexpr uint32_t kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
-        const uint32_t hi0 = __umulhi(kM0, c.x), lo0 = kM0 * c.x;
-        const uint32_t hi1 = __umulhi(kM1, c.z), lo1 = kM1 * c.z;
-        c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
+        // one 32 x 32 -> 64-bit product per word gives both halves (v_mad_u64_u32)
+        const uint64_t p0 = static_cast<uint64_t>(kM0) * c.x, p1 = static_cast<uint64_t>(kM1) * c.z;
+        c = make_uint4(static_cast<uint32_t>(p1 >> 32) ^ c.y ^ k.x, static_cast<uint32_t>(p1),
+                       static_cast<uint32_t>(p0 >> 32) ^ c.w ^ k.y, static_cast<uint32_t>(p0));
         k.x += kW0;
         k.y += kW1;
     }
@@ -900,56 +901,100 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
     if (a.rowwise && lane == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
 }
 
-// Four consecutive columns c0..c0+3 (c0 % 4 == 0) share one Philox call: the same noise
-// sr_noise gives each of them (word (col >> 1) & 3, half col & 1 of the call for col >> 3).
-__device__ __forceinline__ void sr_noise4(uint64_t seed, uint32_t step, uint32_t table,
-                                          uint64_t row, uint32_t c0, uint32_t which,
-                                          uint32_t (&nz)[4]) {
+// C consecutive columns c0 .. c0 + C - 1 (C = 4 or 8, c0 % C == 0) take their noise from one
+// Philox call: the same noise sr_noise gives each of them (word (col >> 1) & 3, half col & 1
+// of the call for col >> 3); eight columns use all four words of the call.
+template <int C>
+__device__ __forceinline__ void sr_noise_cols(uint64_t seed, uint32_t step, uint32_t table,
+                                              uint64_t row, uint32_t c0, uint32_t which,
+                                              uint32_t (&nz)[C]) {
     const uint4 ctr = make_uint4(static_cast<uint32_t>(row), static_cast<uint32_t>(row >> 32), step,
                                  (table << 16) | (which << 14) | (c0 >> 3));
     const uint4 w = philox4x32_10(ctr, make_uint2(static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)));
-    const bool low = ((c0 >> 1) & 3) == 0;
-    const uint32_t wa = low ? w.x : w.z, wb = low ? w.y : w.w;
-    nz[0] = wa & 0xffffu;
-    nz[1] = wa >> 16;
-    nz[2] = wb & 0xffffu;
-    nz[3] = wb >> 16;
-}
-
-__device__ __forceinline__ void load4(const uint8_t *base, int bf16, int64_t e0, float (&x)[4]) {
-    if (bf16) {
-        const u32x2_v v = *as_global(reinterpret_cast<const u32x2_v *>(base + e0 * 2));
-        x[0] = bf16_bits_to_float(static_cast<uint16_t>(v.x));
-        x[1] = bf16_bits_to_float(static_cast<uint16_t>(v.x >> 16));
-        x[2] = bf16_bits_to_float(static_cast<uint16_t>(v.y));
-        x[3] = bf16_bits_to_float(static_cast<uint16_t>(v.y >> 16));
+    uint32_t words[C / 2];
+    if constexpr (C == 8) {
+        words[0] = w.x; words[1] = w.y; words[2] = w.z; words[3] = w.w;
     } else {
-        const f32x4_v v = *as_global(reinterpret_cast<const f32x4_v *>(base + e0 * 4));
-        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        const bool low = ((c0 >> 1) & 3) == 0;
+        words[0] = low ? w.x : w.z;
+        words[1] = low ? w.y : w.w;
     }
-}
-
-__device__ __forceinline__ void store4(uint8_t *base, int bf16, int64_t e0, const float (&x)[4],
-                                       int sr, const uint32_t (&nz)[4]) {
-    if (bf16) {
-        uint32_t h[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            h[e] = sr ? stochastic_bf16_bits(x[e], nz[e]) : float_to_bf16_bits_rne(x[e]);
-        *as_global(reinterpret_cast<u32x2_v *>(base + e0 * 2)) = u32x2_v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    for (int j = 0; j < C; ++j) nz[j] = (words[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+}
+
+// Nontemporal loads and stores: the sparse update reads and writes each touched row once, so
+// its weight, moment and gradient lines are not kept in the caches (where they would only evict
+// other rows' lines); on the update of 196,608 lookups this takes row-wise Adam from 52 to 36
+// us. The 4-byte row-wise second moments and the row ids stay cached: nontemporal access
+// there measured 9 us slower.
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T *p) {
+    return __builtin_nontemporal_load(as_global(p));
+}
+
+template <typename T>
+__device__ __forceinline__ void st_nt(T *p, T v) {
+    __builtin_nontemporal_store(v, as_global(p));
+}
+
+// Columns e0 .. e0 + C - 1 of an fp32 or bf16 array as fp32 (one 8- or 16-byte load for bf16,
+// C / 4 16-byte loads for fp32), nontemporal.
+template <int C, bool BF16>
+__device__ __forceinline__ void load_cols(const uint8_t *base, int64_t e0, float (&x)[C]) {
+    if constexpr (BF16) {
+        uint32_t h[C / 2];
+        if constexpr (C == 8) {
+            const u32x4_v v = ld_nt(reinterpret_cast<const u32x4_v *>(base + e0 * 2));
+            h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
+        } else {
+            const u32x2_v v = ld_nt(reinterpret_cast<const u32x2_v *>(base + e0 * 2));
+            h[0] = v.x; h[1] = v.y;
+        }
+#pragma unroll
+        for (int j = 0; j < C; ++j) x[j] = bf16_bits_to_float(static_cast<uint16_t>(h[j >> 1] >> (16 * (j & 1))));
     } else {
-        *as_global(reinterpret_cast<f32x4_v *>(base + e0 * 4)) = f32x4_v{x[0], x[1], x[2], x[3]};
+#pragma unroll
+        for (int q = 0; q < C / 4; ++q) {
+            const f32x4_v v = ld_nt(reinterpret_cast<const f32x4_v *>(base + (e0 + 4 * q) * 4));
+            x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+        }
     }
 }
 
-// LPR lanes per touched row, four columns per lane (dim = 4 * LPR), 64 / LPR rows per wave:
-// the same update as adam_rows with vector loads, one Philox call per lane per rounded array,
-// and the launch's table list staged in LDS (rows of one wave may belong to different tables).
-template <int LPR>
+template <int C, bool BF16>
+__device__ __forceinline__ void store_cols(uint8_t *base, int64_t e0, const float (&x)[C], int sr,
+                                           const uint32_t (&nz)[C]) {
+    if constexpr (BF16) {
+        uint32_t h[C];
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+            h[j] = sr ? stochastic_bf16_bits(x[j], nz[j]) : float_to_bf16_bits_rne(x[j]);
+        if constexpr (C == 8)
+            st_nt(reinterpret_cast<u32x4_v *>(base + e0 * 2),
+                  u32x4_v{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)});
+        else
+            st_nt(reinterpret_cast<u32x2_v *>(base + e0 * 2), u32x2_v{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+    } else {
+#pragma unroll
+        for (int q = 0; q < C / 4; ++q)
+            st_nt(reinterpret_cast<f32x4_v *>(base + (e0 + 4 * q) * 4),
+                  f32x4_v{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]});
+    }
+}
+
+// LPR lanes per touched row, C columns per lane (dim = C * LPR), 64 / LPR rows per wave: the
+// same update as adam_rows with vector loads, one Philox call per lane per rounded array, and
+// the launch's table list staged in LDS (rows of one wave may belong to different tables). The
+// row's weights and moments are loaded together with its gradient, before the lazy test, so
+// that one memory round trip follows the row id's. The weight dtype (PB: bf16, else fp32) and
+// the second-moment form (RW: one fp32 per row) are template parameters: a run-time branch
+// around each load makes the compiler wait for every load before issuing the next.
+template <int LPR, int C, bool PB, bool RW>
 __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     constexpr int kRowsPerWave = 64 / LPR;
     constexpr int kRowsPerBlock = kRowsPerWave * (kThreads / 64);
-    constexpr int D = 4 * LPR;
+    constexpr int D = C * LPR;
     __shared__ AdamTable s_t[kAdamTables];
     const int tid = threadIdx.x;
     {
@@ -971,17 +1016,27 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
         if (s_t[mid].first <= slot) lo = mid; else hi = mid - 1;
     }
     const AdamTable &t = s_t[lo];
-    const int c0 = 4 * sub;
+    const int c0 = C * sub;
     const int64_t i = slot - t.first;
+    float g[C], p[C], m[C], v[C];
+    load_cols<C, false>(reinterpret_cast<const uint8_t *>(t.grads), i * D + c0, g);
     const int64_t row = *as_global(t.rows + i);
-    float g[4];
-    load4(reinterpret_cast<const uint8_t *>(t.grads), 0, i * D + c0, g);
+    const int64_t e0 = row * D + c0;
+    load_cols<C, PB>(t.param, e0, p);
+    load_cols<C, PB>(t.exp_avg, e0, m);
+    float v0 = 0.f;
+    if constexpr (RW)
+        v0 = *as_global(reinterpret_cast<const float *>(t.exp_avg_sq) + row);
+    else if (a.sq_bf16)
+        load_cols<C, true>(t.exp_avg_sq, e0, v);
+    else
+        load_cols<C, false>(t.exp_avg_sq, e0, v);
     float coef = 1.f;  // gradient clipping (rows.py:224-231): min(max_norm / (norm + 1e-6), 1)
     if (a.sumsq != nullptr) coef = fminf(a.max_norm / (sqrtf(*a.sumsq) + 1e-6f), 1.0f);
     bool any = false;
     float gsq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < C; ++e) {
         if (a.sumsq != nullptr) g[e] *= coef;
         any |= g[e] != 0.f;
         gsq += g[e] * g[e];
@@ -990,44 +1045,43 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     const uint64_t mask = __ballot(any);
     const uint64_t row_bits = LPR == 64 ? mask : (mask >> ((lane / LPR) * LPR)) & ((1ull << (LPR & 63)) - 1);
     if (a.lazy && row_bits == 0ull) return;
-    if (a.rowwise) {
+    if constexpr (RW) {
 #pragma unroll
         for (int off = LPR / 2; off >= 1; off >>= 1) gsq += __shfl_xor(gsq, off, 64);
     }
-    const int64_t e0 = row * D + c0;
-    float p[4], m[4], v[4];
-    load4(t.param, a.param_bf16, e0, p);
-    load4(t.exp_avg, a.param_bf16, e0, m);
     float v_row = 0.f, denom_row = 0.f;
-    if (a.rowwise) {
-        const float v0 = *as_global(reinterpret_cast<const float *>(t.exp_avg_sq) + row);
+    if constexpr (RW) {
         v_row = fmaf(gsq / static_cast<float>(D), a.one_minus_beta2, v0 * a.beta2);
         denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
-    } else {
-        load4(t.exp_avg_sq, a.sq_bf16, e0, v);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < C; ++e) {
         if (a.has_decay) p[e] = p[e] * a.decay;
         m[e] = fmaf(g[e], a.one_minus_beta1, m[e] * a.beta1);
         float denom = denom_row;
-        if (!a.rowwise) {
+        if constexpr (!RW) {
             v[e] = v[e] * a.beta2 + a.one_minus_beta2 * g[e] * g[e];
             denom = sqrtf(v[e]) / t.sqrt_bc2 + a.eps;
         }
         p[e] = p[e] + (t.neg_lr_bc1 * m[e]) / denom;
     }
-    uint32_t nz[4] = {0u, 0u, 0u, 0u};
-    if (!a.rowwise) {
-        if (a.sr && a.sq_bf16) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 2, nz);
-        store4(t.exp_avg_sq, a.sq_bf16, e0, v, a.sr, nz);
+    uint32_t nz[C];
+#pragma unroll
+    for (int e = 0; e < C; ++e) nz[e] = 0u;
+    if constexpr (!RW) {
+        if (a.sq_bf16) {
+            if (a.sr) sr_noise_cols<C>(a.seed, t.step, t.stream_id, row, c0, 2, nz);
+            store_cols<C, true>(t.exp_avg_sq, e0, v, a.sr, nz);
+        } else {
+            store_cols<C, false>(t.exp_avg_sq, e0, v, a.sr, nz);
+        }
     }
-    const bool rnd = a.sr && a.param_bf16;
-    if (rnd) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 0, nz);
-    store4(t.param, a.param_bf16, e0, p, a.sr, nz);
-    if (rnd) sr_noise4(a.seed, t.step, t.stream_id, row, c0, 1, nz);
-    store4(t.exp_avg, a.param_bf16, e0, m, a.sr, nz);
-    if (a.rowwise && sub == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
+    const bool rnd = PB && a.sr;
+    if (rnd) sr_noise_cols<C>(a.seed, t.step, t.stream_id, row, c0, 0, nz);
+    store_cols<C, PB>(t.param, e0, p, a.sr, nz);
+    if (rnd) sr_noise_cols<C>(a.seed, t.step, t.stream_id, row, c0, 1, nz);
+    store_cols<C, PB>(t.exp_avg, e0, m, a.sr, nz);
+    if (RW && sub == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
 }
 
 // Standalone stochastic rounding of n fp32 values; element i uses the noise of (row i / 4096,
@@ -1256,6 +1310,27 @@ extern "C" int me_sumsq(const float *x, int64_t n, float *out, int accumulate, v
     return check_launch("me_sumsq");
 }
 
+template <int C, bool PB, bool RW>
+void launch_adam_vec_k(int lpr, dim3 grid, hipStream_t s, const AdamArgs &a) {
+    switch (lpr) {
+        case 1: hipLaunchKernelGGL((adam_rows_vec<1, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((adam_rows_vec<2, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((adam_rows_vec<4, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((adam_rows_vec<8, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((adam_rows_vec<16, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((adam_rows_vec<32, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        default: hipLaunchKernelGGL((adam_rows_vec<64, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+    }
+}
+
+template <int C>
+void launch_adam_vec(int lpr, bool pb, bool rw, dim3 grid, hipStream_t s, const AdamArgs &a) {
+    if (pb)
+        rw ? launch_adam_vec_k<C, true, true>(lpr, grid, s, a) : launch_adam_vec_k<C, true, false>(lpr, grid, s, a);
+    else
+        rw ? launch_adam_vec_k<C, false, true>(lpr, grid, s, a) : launch_adam_vec_k<C, false, false>(lpr, grid, s, a);
+}
+
 extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const *exp_avgs,
                               void *const *exp_avg_sqs, const int64_t *const *rows,
                               const float *const *grads, const int64_t *n_rows,
@@ -1318,31 +1393,32 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
         a.n_tables = nk;
         a.total = total;
         if (total == 0) continue;
-        // vector path: dim = 4 * lanes-per-row with lanes-per-row a power of two <= 64, and every
-        // row start aligned for 4-element loads
-        const int lpr = dim % 4 == 0 ? dim / 4 : 0;
-        bool vec = lpr >= 1 && lpr <= 64 && (lpr & (lpr - 1)) == 0;
-        const uintptr_t pal = a.param_bf16 ? 8 : 16, val = a.rowwise ? 4 : (a.sq_bf16 ? 8 : 16);
-        for (int q = 0; q < nk && vec; ++q) {
-            const AdamTable &t = a.t[q];
-            vec = reinterpret_cast<uintptr_t>(t.param) % pal == 0 &&
-                  reinterpret_cast<uintptr_t>(t.exp_avg) % pal == 0 &&
-                  reinterpret_cast<uintptr_t>(t.exp_avg_sq) % val == 0 &&
-                  reinterpret_cast<uintptr_t>(t.grads) % 16 == 0;
-        }
+        // vector paths: dim = C * lanes-per-row (C = 8 columns per lane, else 4) with
+        // lanes-per-row a power of two <= 64, and every row start aligned for C-element loads
+        auto fits = [&](int c) {
+            const int lpr = dim % c == 0 ? dim / c : 0;
+            if (lpr < 1 || lpr > 64 || (lpr & (lpr - 1)) != 0) return 0;
+            const uintptr_t pal = a.param_bf16 ? 2 * c : 16, val = a.rowwise ? 4 : (a.sq_bf16 ? 2 * c : 16);
+            for (int q = 0; q < nk; ++q) {
+                const AdamTable &t = a.t[q];
+                if (reinterpret_cast<uintptr_t>(t.param) % pal != 0 ||
+                    reinterpret_cast<uintptr_t>(t.exp_avg) % pal != 0 ||
+                    reinterpret_cast<uintptr_t>(t.exp_avg_sq) % val != 0 ||
+                    reinterpret_cast<uintptr_t>(t.grads) % 16 != 0)
+                    return 0;
+            }
+            return lpr;
+        };
         hipStream_t s = as_stream(stream);
-        if (vec) {
+        const int lpr8 = fits(8), lpr4 = lpr8 ? 0 : fits(4);
+        if (lpr8 || lpr4) {
+            const int lpr = lpr8 ? lpr8 : lpr4;
             const int64_t per_block = (64 / lpr) * (kThreads / 64);
             const dim3 grid(static_cast<unsigned>(ceil_div(total, per_block)));
-            switch (lpr) {
-                case 1: hipLaunchKernelGGL(adam_rows_vec<1>, grid, dim3(kThreads), 0, s, a); break;
-                case 2: hipLaunchKernelGGL(adam_rows_vec<2>, grid, dim3(kThreads), 0, s, a); break;
-                case 4: hipLaunchKernelGGL(adam_rows_vec<4>, grid, dim3(kThreads), 0, s, a); break;
-                case 8: hipLaunchKernelGGL(adam_rows_vec<8>, grid, dim3(kThreads), 0, s, a); break;
-                case 16: hipLaunchKernelGGL(adam_rows_vec<16>, grid, dim3(kThreads), 0, s, a); break;
-                case 32: hipLaunchKernelGGL(adam_rows_vec<32>, grid, dim3(kThreads), 0, s, a); break;
-                default: hipLaunchKernelGGL(adam_rows_vec<64>, grid, dim3(kThreads), 0, s, a); break;
-            }
+            if (lpr8)
+                launch_adam_vec<8>(lpr, a.param_bf16 != 0, a.rowwise != 0, grid, s, a);
+            else
+                launch_adam_vec<4>(lpr, a.param_bf16 != 0, a.rowwise != 0, grid, s, a);
         } else {
             const dim3 grid(static_cast<unsigned>(ceil_div(total, kThreads / 64)));
             hipLaunchKernelGGL(adam_rows, grid, dim3(kThreads), 0, s, a);

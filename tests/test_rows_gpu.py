@@ -167,6 +167,20 @@ def test_sparse_adam_bf16_matches_oracle(rowwise, wd):
         _assert_bf16_close(v, vr)
 
 
+@pytest.mark.parametrize("D", [4, 8, 12, 128, 512])
+@pytest.mark.parametrize("rowwise", [True, False])
+def test_sparse_adam_kernel_shapes_match_oracle(D, rowwise):
+    # 8 columns per lane (D = 8, 128, 512: 1, 16, 64 lanes per row), 4 per lane (D = 4), one
+    # wave per row (D = 12)
+    (p, m, v), (pr, mr, vr) = _adam_case(torch.bfloat16, rowwise, D=D, R=97, n=40)
+    _assert_bf16_close(p, pr, frac=1e-2)
+    _assert_bf16_close(m, mr, frac=1e-2)
+    if rowwise:
+        assert torch.allclose(v, vr, rtol=1e-6, atol=0)
+    else:
+        _assert_bf16_close(v, vr, frac=1e-2)
+
+
 def _assert_fp32_close(got, want, rtol, atol):
     err = (got - want).abs() - rtol * want.abs()
     assert float(err.max()) <= atol, f"max excess {float(err.max()):.3e} over rtol {rtol} + atol {atol}"
