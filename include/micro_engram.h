@@ -32,7 +32,7 @@ extern "C" {
 /* ---- status codes -------------------------------------------------------------------- */
 #define ME_OK 0
 #define ME_ERR_INVALID -1     /* bad argument (shape, size, null pointer, dtype) */
-#define ME_ERR_UNSUPPORTED -2 /* valid request this build has no kernel for */
+#define ME_ERR_UNSUPPORTED -2 /* valid request this library has no kernel for */
 #define ME_ERR_HIP -3         /* the HIP runtime reported an error (launch, stream) */
 #define ME_ERR_WORKSPACE -4   /* workspace missing or smaller than *_workspace_size */
 

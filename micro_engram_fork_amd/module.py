@@ -165,7 +165,7 @@ class MicroEngram(nn.Module):
                    pin_memory=False):
         """Keep only `rank`'s rows of every table (module.py:115-138). On one GPU (world 1) this
         is every row; the HIP lookup serves it directly. More ranks need the row exchange of
-        micro_engram/rows.py, which this build does not provide."""
+        micro_engram/rows.py, which this package does not provide."""
         spans = [_row_range(rows, rank, world) for rows in self.table_rows]
         pers = [-(-rows // world) for rows in self.table_rows]
         if "tables" in self._modules:

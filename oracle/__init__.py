@@ -1,8 +1,8 @@
 """CPU oracle of the Engram lookup path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package,
-and only as the checker (or the timed CPU baseline) of the HIP path. The product package never
-imports it.
+and only as the expected result the HIP path is tested against (or as the timed CPU baseline).
+The product package never imports it.
 
 Contents (each function cites the reference code it restates):
   hash_oracle.c / engram.py   mults, hash_ids, hash_prev (integer, bit-exact)

@@ -1,6 +1,7 @@
 /*
  * CPU oracle -- TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load this library, and only as the checker of the HIP path.
+ * cpu_baseline leg may load this library, and only as the expected result the HIP path is
+ * tested against.
  *
  * Plain-C restatement of the integer half of micro-engram's Engram lookup path:
  *   oracle_mt19937      the Mersenne Twister MT19937 (Matsumoto & Nishimura 1998), the engine
