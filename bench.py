@@ -325,7 +325,8 @@ def main():
             "copy_1gib_gbs": copy_gbs,
         },
         "roofline_gate": {
-            "kernel": "K/V projection + gate + residual (gate_kernel key + value passes, alpha)",
+            "kernel": "K/V projection + gate + residual (gate224_kernel key + value passes on 256 x 224 "
+                      "tiles, alpha)",
             "bound": "mfma",
             "achieved": gate_tflops,
             "peak": BF16_PEAK_TFLOPS,

@@ -37,7 +37,8 @@
 // 256-byte row segment. The key pass reduces its three sums per row across the 16 lanes with
 // DPP row shifts and combines the two column waves in LDS. Workgroup ids are remapped so the
 // 32 CUs of one XCD work on a compact group of tiles (8 token tiles x 4 column tiles) and share
-// their operands in that XCD's L2.
+// their operands in that XCD's L2. bf16 forward passes run the same scheme on 256 x 224 tiles
+// of 16x16x32 MFMAs (gate224_kernel: whole rounds of tiles on the Gemma-scale shape).
 #include "me_common.h"
 
 #include <type_traits>
@@ -236,10 +237,7 @@ __device__ __forceinline__ float gate_alpha(float sx2, float sk2, float sck, con
     return 1.0f / (1.0f + expf(-s));
 }
 
-// PF: the epilogue's hidden rows (and the key pass's scales) are loaded into registers under
-// the last k-slabs, so their latency and the HBM burst of every CU reaching its epilogue at
-// once overlap the MFMAs (bf16 tiles and hidden under 2 GiB: 32 rows x 16 bytes per lane).
-template <typename T, typename H, int PHASE, bool PF>
+template <typename T, typename H, int PHASE>
 __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kRingBytes];
 
@@ -275,48 +273,15 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
         for (int c = 0; c < 3; ++c) coef_reg[c] = a.tok_coef[(n0 + tid) * 3 + c];
     }
 
-    // ---- epilogue row walk geometry (the prefetch below uses it): 16 lanes x 16 bytes per token
-    // row, lane l16 owning kLaneCols columns, rows rsub, rsub + 4, ... of the wave's 128
+    // ---- epilogue row walk geometry: 16 lanes x 16 bytes per token row, lane l16 owning
+    // kLaneCols columns, rows rsub, rsub + 4, ... of the wave's 128
     constexpr int kPasses = sizeof(T) == 2 ? 1 : 2;
     constexpr int kPassCols = 128 / kPasses;     // columns staged per pass
     constexpr int kLaneCols = 16 / sizeof(T);    // columns per lane in the row walk (8 / 4)
     constexpr int kRowWords = kLaneCols * sizeof(H) / 4;  // hidden words per lane per row
     constexpr int kBatch = kRowWords <= 4 ? 32 : 16;      // rows whose hidden loads are in flight
-    static_assert(!PF || (kPasses == 1 && kRowWords == 4 && kBatch == 32), "prefetch geometry");
     const int l16 = lane & 15, rsub = lane >> 4;
     const int64_t ntok0 = n0 + wn * 128;          // first token of the wave
-    // prefetched epilogue operands: 32 hidden rows, and (key pass) 2 x 2 words of the scale
-    // deltas (bf16 deltas use the first of each pair); every load is issued for every lane
-    // (out-of-range offsets read zeros), so their number is fixed
-    constexpr int kPfLoads = 32 + (PHASE == kKey ? 4 : 0);
-    u32x4_v xpre[PF ? 32 : 1];
-    u32x4_v spre[PF && PHASE == kKey ? 4 : 1];
-    auto prefetch = [&]() {
-        if constexpr (PF) {
-            const int64_t jl = j0 + wj * 128 + l16 * kLaneCols;
-            const bool jok = jl < a.d;
-            const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
-#pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                const int64_t n = ntok0 + u * 4 + rsub;
-                const uint32_t off = jok && n < a.n ? static_cast<uint32_t>((n * a.d + jl) * 2) : a.hidden_bytes;
-                xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0));
-            }
-            if constexpr (PHASE == kKey) {
-                const int esz = a.scale_bf16 ? 2 : 4;
-                const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
-                const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
-                const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
-                spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
-                spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
-                spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-                spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
-            }
-        }
-    };
 
     // ---- K loop over 128-byte slabs: A_s (W rows) in unit 2s % 5, B_s (mem rows) in (2s+1) % 5
     const uint32_t row_bytes = static_cast<uint32_t>(a.m * sizeof(T));
@@ -380,12 +345,6 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     // B_{s+2} and the reads of slab s+1's first fragments (the parts its first MFMAs need
     // come first). sched_barrier pins this order.
     constexpr int kFragOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};  // a0, b0..b3, a1..a3
-    // The slab loop is peeled around the prefetch, which goes out at the end of slab pf_at,
-    // right behind the last real slab's loads (B_{slabs-1}). The slabs after it issue no
-    // loads (all theirs would be past the end), so the prefetched registers share the tail
-    // only with the fragments, and the slab after it waits for its slab behind the prefetch.
-    const int pf_at = PF ? max(slabs - 3, 0) : slabs;
-    static_assert(kPfLoads <= 63, "vmcnt counts up to 63");
     auto slab = [&](int sl, auto wait, auto dma) {
         const uint8_t *ua = unit_a(sl), *ub = unit_b(sl);
 #pragma unroll
@@ -424,10 +383,8 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             mfma_xy(f1, acc, i >> 2, i & 3);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // slab s+1 landed: A_{s+2} (or, in the slab after the prefetch, the prefetch) may still
-        // fly; past the last slab there is nothing to wait for
+        // slab s+1 landed: A_{s+2} may still fly
         if constexpr (decltype(wait)::value == 1) wait_vmcnt<kDmaPerOperand>();
-        if constexpr (decltype(wait)::value == 2) wait_vmcnt<kPfLoads>();
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t *na = unit_a(sl + 1), *nb = unit_b(sl + 1);
@@ -447,17 +404,8 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
         }
     };
     using WaitSlab = std::integral_constant<int, 1>;
-    using WaitPrefetch = std::integral_constant<int, 2>;
-    using NoWait = std::integral_constant<int, 0>;
     using Dma = std::true_type;
-    using NoDma = std::false_type;
-    for (int sl = 0; sl < pf_at; ++sl) slab(sl, WaitSlab{}, Dma{});
-    if constexpr (PF) {
-        slab(pf_at, WaitSlab{}, Dma{});
-        prefetch();
-        if (pf_at + 1 < slabs) slab(pf_at + 1, WaitPrefetch{}, NoDma{});
-        for (int sl = pf_at + 2; sl < slabs; ++sl) slab(sl, NoWait{}, NoDma{});
-    }
+    for (int sl = 0; sl < slabs; ++sl) slab(sl, WaitSlab{}, Dma{});
     wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
     __syncthreads();  // the ring is free for the epilogue
 
@@ -513,22 +461,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 #pragma unroll
         for (int e = 0; e < kLaneCols; ++e) wcol[e] = 1.f;
         constexpr bool kScaled = PHASE == kKey || PHASE == kGradKey;
-        if (PF && PHASE == kKey && jok && a.q_delta != nullptr) {
-            const uint32_t *qw = reinterpret_cast<const uint32_t *>(&spre[0]);
-            const uint32_t *kw = reinterpret_cast<const uint32_t *>(&spre[2]);
-#pragma unroll
-            for (int e = 0; e < kLaneCols; ++e) {
-                float qv, kv;
-                if (a.scale_bf16) {
-                    qv = bf16_bits_to_float(static_cast<uint16_t>(qw[e / 2] >> (16 * (e & 1))));
-                    kv = bf16_bits_to_float(static_cast<uint16_t>(kw[e / 2] >> (16 * (e & 1))));
-                } else {
-                    qv = __uint_as_float(qw[e]);
-                    kv = __uint_as_float(kw[e]);
-                }
-                wcol[e] = (1.f + qv) * (1.f + kv);
-            }
-        } else if (kScaled && jok && a.q_delta != nullptr) {
+        if (kScaled && jok && a.q_delta != nullptr) {
             float qv[kLaneCols], kv[kLaneCols];
             if (a.scale_bf16) {
                 load_run<uint16_t, kLaneCols>(static_cast<const uint8_t *>(a.q_delta) + jl * 2, qv);
@@ -554,10 +487,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
             for (int u = 0; u < kRowBatch; ++u) {
                 const int row = (b0 + u) * 4 + rsub;
                 const int64_t n = ntok0 + row;
-                if constexpr (PF) {
-#pragma unroll
-                    for (int q = 0; q < kRowWords; ++q) xr[u][q] = xpre[u][q];
-                } else if (jok && n < a.n) {
+                if (jok && n < a.n) {
                     const int64_t off = (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
 #pragma unroll
                     for (int q = 0; q < kRowWords; q += 2) {
@@ -717,6 +647,357 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
     }
 }
 
+// ---- 224-column tiles: bf16 forward passes on 16x16x32 MFMAs ------------------------------------
+// The forward passes for bf16 engrams and bf16 hidden states (under 2 GiB) run on 256 (tokens) x
+// 224 (columns) tiles; gate_kernel serves every other case. On the Gemma-scale shape (d 5376 =
+// 24 x 224, 8192 tokens) that is 768 tiles, three full rounds of 256 CUs, where 256 x 256 tiles
+// make 672 and leave 96 CUs idle in the third round. Each wave owns 128 tokens x 112 columns as
+// 7 x 8 tiles of v_mfma_f32_16x16x32_bf16 (224 accumulators); a slab is two 32-wide k-steps. A
+// slab's 224 W rows take 7 row loads per wave, its 256 mem rows 8. The ring, the swizzle, the
+// load/barrier order and the epilogue follow gate_kernel. Under the last three slabs the
+// workgroup also loads the first 16 of each lane's 32 hidden rows (and the key pass's scale
+// deltas) into registers, so their latency and the HBM burst of every CU reaching its epilogue
+// at once overlap the MFMAs; the other 16 rows are loaded as the K loop ends.
+constexpr int kTJ = 224;                // output columns per tile
+constexpr int kWJ = kTJ / 2;            // columns per wave (112)
+constexpr int kSubJ = kWJ / 16;         // 16-row A subtiles per wave (7)
+constexpr int kSubN = 128 / 16;         // 16-row B subtiles per wave (8)
+constexpr int kDmaA = kTJ / (8 * 4);    // A row loads per wave per slab (7)
+constexpr int kDmaB = kTile / (8 * 4);  // B row loads per wave per slab (8)
+constexpr int kParts = kSubJ + kSubN;   // fragment parts per k-step (15)
+constexpr int kPitch16 = kWJ * 2 + 8;   // staged token row: 224 B + pad
+constexpr int kWaveStage16 = 128 * kPitch16;
+static_assert(4 * kWaveStage16 + 2 * kTile * 3 * 4 <= kRingBytes, "epilogue must fit in the ring");
+static_assert(kTJ * kSlab <= kUnit, "a slab's W rows fit a ring unit");
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct Frag16 {
+    bf16x8 a[kSubJ], b[kSubN];
+};
+
+__device__ __forceinline__ float acc_read4(const floatx4 &t, int e) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(t[e]));
+    return v;
+}
+
+// Part p of a k-step's fragments (A subtile p for p < 7, else B subtile p - 7): lane l reads row
+// (l & 15) of the subtile at logical chunk 4 ks + (l >> 4) (8 of the k-step's 32 k values; the
+// same lanes carry the same k values for A and B).
+__device__ __forceinline__ void load_part16(const uint8_t *ua, const uint8_t *ub, int ks, int wj, int wn,
+                                            int lane, Frag16 &f, int p) {
+    const int r = lane & 15;
+    if (p < kSubJ) {
+        const int row = wj * kWJ + p * 16 + r;
+        const int c = ((4 * ks + (lane >> 4)) ^ ((row >> 1) & 7)) << 4;
+        f.a[p] = *reinterpret_cast<const bf16x8 *>(ua + row * kSlab + c);
+    } else {
+        const int row = wn * 128 + (p - kSubJ) * 16 + r;
+        const int c = ((4 * ks + (lane >> 4)) ^ ((row >> 1) & 7)) << 4;
+        f.b[p - kSubJ] = *reinterpret_cast<const bf16x8 *>(ub + row * kSlab + c);
+    }
+}
+
+template <int PHASE>
+__global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) {
+    using T = uint16_t;
+    using H = uint16_t;
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kRingBytes];
+
+    // ---- tile of this workgroup: XCD-compact groups of 8 token tiles x all column tiles
+    const int bid = blockIdx.x;
+    const int logical = (bid % kXcds) * a.per_xcd + bid / kXcds;
+    if (logical >= a.total_tiles) return;
+    const int group_size = kGroupTiles * a.n_jt;
+    const int group = logical / group_size;
+    const int in_group = logical - group * group_size;
+    const int first_nt = group * kGroupTiles;
+    const int group_nts = min(kGroupTiles, a.n_nt - first_nt);
+    const int nt = first_nt + in_group % group_nts;
+    const int jt = in_group / group_nts;
+    const int64_t j0 = static_cast<int64_t>(jt) * kTJ;
+    const int64_t n0 = static_cast<int64_t>(nt) * kTile;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wj = wave >> 1, wn = wave & 1;
+
+    float alpha_reg = 0.f;
+    if (PHASE == kValue && n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
+
+    // ---- epilogue row walk geometry: 14 of 16 lanes x 16 bytes per token row (the wave's 112
+    // columns), lane l16 owning 8 columns, rows rsub, rsub + 4, ... of the wave's 128 tokens
+    constexpr int kLaneCols = 8;
+    const int l16 = lane & 15, rsub = lane >> 4;
+    const int64_t ntok0 = n0 + wn * 128;
+    const int64_t jl = j0 + wj * kWJ + l16 * kLaneCols;  // lane's first column
+    const bool jok = l16 < kWJ / kLaneCols && jl < a.d;  // d is a multiple of 8
+    // hidden rows 0..kPfRows-1 are loaded under the last slabs, the rest at the epilogue start
+    constexpr int kPfRows = 16;
+    constexpr int kPfLoads = kPfRows + (PHASE == kKey ? 4 : 0);
+    u32x4_v xpre[32];
+    u32x4_v spre[PHASE == kKey ? 4 : 1];
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+    auto load_rows = [&](int u0, int u1) {
+#pragma unroll
+        for (int u = u0; u < u1; ++u) {
+            const int64_t n = ntok0 + u * 4 + rsub;
+            const uint32_t off = jok && n < a.n ? static_cast<uint32_t>((n * a.d + jl) * 2) : a.hidden_bytes;
+            xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0));
+        }
+    };
+    auto prefetch = [&]() {
+        load_rows(0, kPfRows);
+        if constexpr (PHASE == kKey) {
+            const int esz = a.scale_bf16 ? 2 : 4;
+            const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
+            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+            spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+            spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
+            spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+            spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+        }
+    };
+
+    // ---- K loop over 128-byte slabs: A_s (W rows) in unit 2s % 5, B_s (mem rows) in (2s+1) % 5
+    const uint32_t row_bytes = static_cast<uint32_t>(a.m * sizeof(T));
+    const int slabs = static_cast<int>(ceil_div(row_bytes, kSlab));
+    const int32x4 rsrc_w = buffer_rsrc(a.w, a.w_bytes);
+    const int32x4 rsrc_m = buffer_rsrc(a.mem, a.mem_bytes);
+    // A load i of a wave fills rows 8 (7 wave + i) + [0, 8), B load i rows 8 (8 wave + i) + [0, 8):
+    // lane l writes row + l / 8 at physical chunk l % 8 (logical chunk (l % 8) ^ ((row >> 1) & 7))
+    uint32_t offw[kDmaA], offm[kDmaB];
+    bool okw[kDmaA], okm[kDmaB];
+    uint32_t chw[kDmaA], chm[kDmaB];
+#pragma unroll
+    for (int i = 0; i < kDmaA; ++i) {
+        const int row = (wave * kDmaA + i) * 8 + (lane >> 3);
+        chw[i] = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
+        okw[i] = j0 + row < a.d;
+        offw[i] = okw[i] ? static_cast<uint32_t>(j0 + row) * row_bytes + chw[i] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kDmaB; ++i) {
+        const int row = (wave * kDmaB + i) * 8 + (lane >> 3);
+        chm[i] = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
+        okm[i] = n0 + row < a.n;
+        offm[i] = okm[i] ? static_cast<uint32_t>(n0 + row) * row_bytes + chm[i] : 0u;
+    }
+    const uint32_t ring_lds = lds_addr(ring);
+    auto issue_a = [&](int sl, int i) {
+        const uint32_t kb = static_cast<uint32_t>(sl) * kSlab;
+        const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl) % kUnits) * kUnit +
+                             static_cast<uint32_t>(wave * kDmaA + i) * 1024u;
+        dma16(rsrc_w, __builtin_amdgcn_readfirstlane(dst), okw[i] && kb + chw[i] < row_bytes ? offw[i] + kb : a.w_bytes);
+    };
+    auto issue_b = [&](int sl, int i) {
+        const uint32_t kb = static_cast<uint32_t>(sl) * kSlab;
+        const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl + 1) % kUnits) * kUnit +
+                             static_cast<uint32_t>(wave * kDmaB + i) * 1024u;
+        dma16(rsrc_m, __builtin_amdgcn_readfirstlane(dst), okm[i] && kb + chm[i] < row_bytes ? offm[i] + kb : a.mem_bytes);
+    };
+    auto unit_a = [&](int sl) { return ring + ((2 * sl) % kUnits) * kUnit; };
+    auto unit_b = [&](int sl) { return ring + ((2 * sl + 1) % kUnits) * kUnit; };
+    floatx4 acc[kSubJ][kSubN];
+#pragma unroll
+    for (int x = 0; x < kSubJ; ++x)
+#pragma unroll
+        for (int y = 0; y < kSubN; ++y)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[x][y][e] = 0.f;
+
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+        for (int i = 0; i < kDmaA; ++i) issue_a(sl, i);
+#pragma unroll
+        for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
+    }
+    wait_vmcnt<kDmaA + kDmaB>();  // A_0, B_0 landed (A_1, B_1 may fly)
+    __syncthreads();
+    Frag16 f0, f1;
+    // fragment parts in the order the next k-step's MFMAs use them: a0, b0..b7, a1..a6
+    auto part_of = [](int q) { return q == 0 ? 0 : (q <= kSubN ? kSubJ + q - 1 : q - kSubN); };
+#pragma unroll
+    for (int q = 0; q < kParts; ++q) load_part16(unit_a(0), unit_b(0), 0, wj, wn, lane, f0, part_of(q));
+
+    constexpr int kMfma = kSubJ * kSubN;  // 56 per k-step
+    const int pf_at = max(slabs - 3, 0);
+    static_assert(kPfLoads + kDmaA + kDmaB <= 63, "vmcnt counts up to 63");
+    // Slab s: k-step 0 issues A_{s+2} (into B_{s-1}'s unit, free since the previous barrier) and
+    // reads k-step 1's fragments; k-step 1 waits for slab s+1 after its first 8 MFMAs, passes
+    // the barrier, then issues B_{s+2} (into A_s's unit) and reads slab s+1's first fragments.
+    auto slab = [&](int sl, auto wait, auto dma) {
+        const uint8_t *ua = unit_a(sl), *ub = unit_b(sl);
+#pragma unroll
+        for (int i = 0; i < kMfma; ++i) {
+            acc[i / kSubN][i % kSubN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                f0.a[i / kSubN], f0.b[i % kSubN], acc[i / kSubN][i % kSubN], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (decltype(dma)::value && i < kDmaA) {
+                issue_a(sl + 2, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (i % 3 == 2 && i / 3 < kParts) {
+                load_part16(ua, ub, 1, wj, wn, lane, f1, part_of(i / 3));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        constexpr int kPre = 8;  // MFMAs of k-step 1 before the wait and the barrier
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+            acc[i / kSubN][i % kSubN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                f1.a[i / kSubN], f1.b[i % kSubN], acc[i / kSubN][i % kSubN], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // slab s+1 landed: A_{s+2} (or, in the slab after the prefetch, the prefetch) may still
+        // fly; past the last slab there is nothing to wait for
+        if constexpr (decltype(wait)::value == 1) wait_vmcnt<kDmaA>();
+        if constexpr (decltype(wait)::value == 2) wait_vmcnt<kPfLoads>();
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *na = unit_a(sl + 1), *nb = unit_b(sl + 1);
+#pragma unroll
+        for (int i = kPre; i < kMfma; ++i) {
+            acc[i / kSubN][i % kSubN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                f1.a[i / kSubN], f1.b[i % kSubN], acc[i / kSubN][i % kSubN], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            const int q = i - kPre;
+            if (decltype(dma)::value && q < kDmaB) {
+                issue_b(sl + 2, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (q % 2 == 1 && q / 2 < kParts) {  // past the last slab these read a stale unit; unused
+                load_part16(na, nb, 0, wj, wn, lane, f0, part_of(q / 2));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    using WaitSlab = std::integral_constant<int, 1>;
+    using WaitPrefetch = std::integral_constant<int, 2>;
+    using NoWait = std::integral_constant<int, 0>;
+    using Dma = std::true_type;
+    using NoDma = std::false_type;
+    for (int sl = 0; sl < pf_at; ++sl) slab(sl, WaitSlab{}, Dma{});
+    slab(pf_at, WaitSlab{}, Dma{});
+    prefetch();
+    if (pf_at + 1 < slabs) slab(pf_at + 1, WaitPrefetch{}, NoDma{});
+    for (int sl = pf_at + 2; sl < slabs; ++sl) slab(sl, NoWait{}, NoDma{});
+    wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
+    __syncthreads();  // the ring is free for the epilogue
+    load_rows(kPfRows, 32);
+
+    // ---- epilogue: each wave stages round_T of its 128 x 112 tile as [token][column] rows
+    uint8_t *stage = ring + wave * kWaveStage16;
+    float *s_aux = reinterpret_cast<float *>(ring + 4 * kWaveStage16);  // key [2][256][3]; value [256]
+    if (PHASE == kValue) {
+        s_aux[tid] = alpha_reg;
+    } else {
+        for (int e = tid; e < 2 * kTile * 3; e += kThreads) s_aux[e] = 0.f;
+    }
+    // acc[x][y][e] is column 16x + 4 (lane >> 4) + e of token 16y + (lane & 15)
+    {
+        const int tr = lane & 15, cq = lane >> 4;
+#pragma unroll
+        for (int x = 0; x < kSubJ; ++x)
+#pragma unroll
+            for (int y = 0; y < kSubN; ++y) {
+                uint32_t w[2];
+                T *tv = reinterpret_cast<T *>(w);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tv[e] = from_f<T>(acc_read4(acc[x][y], e));
+                *reinterpret_cast<uint2 *>(stage + (16 * y + tr) * kPitch16 + (16 * x + 4 * cq) * 2) =
+                    make_uint2(w[0], w[1]);
+                if (y == kSubN - 1) __builtin_amdgcn_sched_barrier(0);
+            }
+    }
+    __syncthreads();  // staging (and s_aux) visible
+
+    float wcol[kLaneCols];  // q_scale * k_scale of the lane's columns (key pass)
+#pragma unroll
+    for (int e = 0; e < kLaneCols; ++e) wcol[e] = 1.f;
+    if (PHASE == kKey && jok && a.q_delta != nullptr) {
+        const uint32_t *qw = reinterpret_cast<const uint32_t *>(&spre[0]);
+        const uint32_t *kw = reinterpret_cast<const uint32_t *>(&spre[2]);
+#pragma unroll
+        for (int e = 0; e < kLaneCols; ++e) {
+            float qv, kv;
+            if (a.scale_bf16) {
+                qv = bf16_bits_to_float(static_cast<uint16_t>(qw[e / 2] >> (16 * (e & 1))));
+                kv = bf16_bits_to_float(static_cast<uint16_t>(kw[e / 2] >> (16 * (e & 1))));
+            } else {
+                qv = __uint_as_float(qw[e]);
+                kv = __uint_as_float(kw[e]);
+            }
+            wcol[e] = (1.f + qv) * (1.f + kv);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+        const int row = u * 4 + rsub;
+        const int64_t n = ntok0 + row;
+        uint32_t cw[4] = {0u, 0u, 0u, 0u};
+        if (l16 < kWJ / kLaneCols) {
+            const uint8_t *sp = stage + row * kPitch16 + l16 * 16;
+            const uint2 c0 = reinterpret_cast<const uint2 *>(sp)[0];
+            const uint2 c1 = reinterpret_cast<const uint2 *>(sp)[1];
+            cw[0] = c0.x; cw[1] = c0.y; cw[2] = c1.x; cw[3] = c1.y;
+        }
+        const T *cv = reinterpret_cast<const T *>(cw);
+        const u32x4_v xq = xpre[u];
+        uint32_t xw[4] = {xq[0], xq[1], xq[2], xq[3]};
+        const H *xv = reinterpret_cast<const H *>(xw);
+        if constexpr (PHASE == kKey) {
+            float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < kLaneCols; ++e) {
+                const float kv = to_f<T>(cv[e]);
+                const float x = to_f<H>(xv[e]);
+                sk2 += kv * kv;
+                sck += x * wcol[e] * kv;
+                sx2 += x * x;
+            }
+            sk2 = row16_sum(sk2);
+            sck = row16_sum(sck);
+            sx2 = row16_sum(sx2);
+            if (l16 == 15) {
+                float *p = s_aux + (wj * kTile + wn * 128 + row) * 3;
+                p[0] = sk2;
+                p[1] = sck;
+                p[2] = sx2;
+            }
+        } else {
+            if (jok && n < a.n) {
+                const float alpha = s_aux[wn * 128 + row];
+                uint32_t ow[4];
+                H *ov = reinterpret_cast<H *>(ow);
+#pragma unroll
+                for (int e = 0; e < kLaneCols; ++e)
+                    ov[e] = from_f<H>(to_f<H>(xv[e]) + round_t<H>(alpha * to_f<T>(cv[e])));
+                uint8_t *p = a.out + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
+                __builtin_nontemporal_store(u32x2_t{ow[0], ow[1]}, reinterpret_cast<u32x2_t *>(p));
+                __builtin_nontemporal_store(u32x2_t{ow[2], ow[3]}, reinterpret_cast<u32x2_t *>(p) + 1);
+            }
+        }
+    }
+    if constexpr (PHASE == kKey) {
+        __syncthreads();  // s_aux complete
+        const int64_t n = n0 + tid;
+        if (n < a.n) {
+            const float *p0 = s_aux + tid * 3;
+            const float *p1 = s_aux + (kTile + tid) * 3;
+            float *o = a.partials + (static_cast<int64_t>(jt) * a.n + n) * 3;
+            o[0] = p0[0] + p1[0];
+            o[1] = p0[1] + p1[1];
+            o[2] = p0[2] + p1[2];
+        }
+    }
+}
+
 // Gate of every token from the key pass's partial sums, summed in column-tile order (so the
 // result does not depend on scheduling); keep = false zeroes the gate.
 __global__ __launch_bounds__(kThreads) void gate_alpha_kernel(const GateArgs a) {
@@ -796,8 +1077,10 @@ __global__ __launch_bounds__(kThreads) void gate_grad_scale_kernel(const GateArg
     grad_k[j] = (1.f + q) * pj;
 }
 
+// [n_jt][n][3] partial sums for the narrower (224-column) tiles, which also hold the 256-column
+// tiles' ([ceil(d / 224) >= ceil(d / 256)]), then [n] gates
 size_t workspace_bytes(int64_t n, int64_t d) {
-    return (static_cast<size_t>(ceil_div(d, kTile)) * 3 + 1) * static_cast<size_t>(n) * sizeof(float);
+    return (static_cast<size_t>(ceil_div(d, kTJ)) * 3 + 1) * static_cast<size_t>(n) * sizeof(float);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -909,7 +1192,7 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     a.alpha_out = alpha_out;
     a.row_stats_out = row_stats;
     a.partials = static_cast<float *>(workspace);
-    a.alpha_eff = a.partials + ceil_div(model_dim, kTile) * 3 * n;
+    a.alpha_eff = a.partials + ceil_div(model_dim, kTJ) * 3 * n;
     const int64_t hidden_bytes = n * model_dim * static_cast<int64_t>(dtype_size(hidden_dtype));
     // the prefetching kernels address hidden with 32-bit buffer offsets
     const bool prefetch = dtype == ME_BF16 && hidden_dtype == ME_BF16 &&
@@ -922,27 +1205,42 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     ak.w = static_cast<const uint8_t *>(w_key);
     av.w = static_cast<const uint8_t *>(w_value);
     const dim3 grid(static_cast<unsigned>(a.per_xcd * kXcds));
-#define ME_GATE_LAUNCH(T, H, PF)                                                                 \
+#define ME_GATE_LAUNCH(T, H)                                                                     \
     do {                                                                                         \
-        hipLaunchKernelGGL((gate_kernel<T, H, kKey, PF>), grid, dim3(kThreads), 0, s, ak);      \
+        hipLaunchKernelGGL((gate_kernel<T, H, kKey>), grid, dim3(kThreads), 0, s, ak);          \
         int st_ = check_launch("me_gate_residual (key pass)");                                  \
         if (st_ != ME_OK) return st_;                                                            \
         hipLaunchKernelGGL(gate_alpha_kernel, dim3(static_cast<unsigned>(ceil_div(n, kThreads))), \
                            dim3(kThreads), 0, s, ak);                                            \
         st_ = check_launch("me_gate_residual (gate)");                                           \
         if (st_ != ME_OK) return st_;                                                            \
-        hipLaunchKernelGGL((gate_kernel<T, H, kValue, PF>), grid, dim3(kThreads), 0, s, av);    \
+        hipLaunchKernelGGL((gate_kernel<T, H, kValue>), grid, dim3(kThreads), 0, s, av);        \
         return check_launch("me_gate_residual (value pass)");                                   \
     } while (0)
     if (dtype == ME_BF16) {
-        if (hidden_dtype == ME_BF16) {
-            if (prefetch) ME_GATE_LAUNCH(uint16_t, uint16_t, true);
-            ME_GATE_LAUNCH(uint16_t, uint16_t, false);
+        if (hidden_dtype == ME_BF16 && prefetch) {
+            // 256 x 224 tiles (16x16x32 MFMAs)
+            ak.n_jt = av.n_jt = static_cast<int>(ceil_div(model_dim, kTJ));
+            ak.total_tiles = av.total_tiles = ak.n_jt * ak.n_nt;
+            ak.per_xcd = av.per_xcd = static_cast<int>(ceil_div(ak.total_tiles, kXcds));
+            const dim3 grid16(static_cast<unsigned>(ak.per_xcd * kXcds));
+            hipLaunchKernelGGL(gate224_kernel<kKey>, grid16, dim3(kThreads), 0, s, ak);
+            int st_ = check_launch("me_gate_residual (key pass)");
+            if (st_ != ME_OK) return st_;
+            hipLaunchKernelGGL(gate_alpha_kernel, dim3(static_cast<unsigned>(ceil_div(n, kThreads))),
+                               dim3(kThreads), 0, s, ak);
+            st_ = check_launch("me_gate_residual (gate)");
+            if (st_ != ME_OK) return st_;
+            hipLaunchKernelGGL(gate224_kernel<kValue>, grid16, dim3(kThreads), 0, s, av);
+            return check_launch("me_gate_residual (value pass)");
         }
-        ME_GATE_LAUNCH(uint16_t, float, false);
+        if (hidden_dtype == ME_BF16) {
+            ME_GATE_LAUNCH(uint16_t, uint16_t);
+        }
+        ME_GATE_LAUNCH(uint16_t, float);
     }
-    if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(float, uint16_t, false);
-    ME_GATE_LAUNCH(float, float, false);
+    if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(float, uint16_t);
+    ME_GATE_LAUNCH(float, float);
 #undef ME_GATE_LAUNCH
 }
 
@@ -1008,13 +1306,13 @@ extern "C" int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n,
     const dim3 tok_grid(static_cast<unsigned>(ceil_div(n, kThreads)));
 #define ME_GATE_GRAD_LAUNCH(T, H)                                                                \
     do {                                                                                         \
-        hipLaunchKernelGGL((gate_kernel<T, H, kGradValue, false>), grid, dim3(kThreads), 0, s, av); \
+        hipLaunchKernelGGL((gate_kernel<T, H, kGradValue>), grid, dim3(kThreads), 0, s, av);    \
         int st_ = check_launch("me_gate_backward (value side)");                                \
         if (st_ != ME_OK) return st_;                                                            \
         hipLaunchKernelGGL(gate_grad_token_kernel, tok_grid, dim3(kThreads), 0, s, a);           \
         st_ = check_launch("me_gate_backward (token coefficients)");                             \
         if (st_ != ME_OK) return st_;                                                            \
-        hipLaunchKernelGGL((gate_kernel<T, H, kGradKey, false>), grid, dim3(kThreads), 0, s, ak); \
+        hipLaunchKernelGGL((gate_kernel<T, H, kGradKey>), grid, dim3(kThreads), 0, s, ak);      \
         st_ = check_launch("me_gate_backward (key side)");                                       \
         if (st_ != ME_OK) return st_;                                                            \
     } while (0)
