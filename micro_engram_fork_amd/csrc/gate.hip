@@ -158,6 +158,16 @@ __device__ __forceinline__ void dma16(const int32x4 &rsrc, uint32_t lds_base, ui
                  : "memory");
 }
 
+// The same with a uniform byte offset soffset added to every lane's voffset (the buffer's range
+// check looks at voffset, so an out-of-range voffset still reads zeros).
+__device__ __forceinline__ void dma16_so(const int32x4 &rsrc, uint32_t lds_base, uint32_t voffset,
+                                         uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
@@ -769,36 +779,36 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     const int32x4 rsrc_w = buffer_rsrc(a.w, a.w_bytes);
     const int32x4 rsrc_m = buffer_rsrc(a.mem, a.mem_bytes);
     // A load i of a wave fills rows 8 (7 wave + i) + [0, 8), B load i rows 8 (8 wave + i) + [0, 8):
-    // lane l writes row + l / 8 at physical chunk l % 8 (logical chunk (l % 8) ^ ((row >> 1) & 7))
+    // lane l writes row + l / 8 at physical chunk l % 8 (logical chunk (l % 8) ^ ((row >> 1) & 7)).
+    // A lane's byte offset of each load is fixed for the whole K loop (out-of-range rows: the
+    // buffer size, which reads zeros); the slab's offset goes in the scalar offset, and the LDS
+    // destination is computed on scalars, so a load costs a few scalar instructions between two
+    // 16-cycle MFMAs. Every slab issued is a whole one (row_bytes % 128 == 0, at least 3 slabs,
+    // so the peeled tail issues none past the end).
+    const uint32_t wave_s = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wave));
     uint32_t offw[kDmaA], offm[kDmaB];
-    bool okw[kDmaA], okm[kDmaB];
-    uint32_t chw[kDmaA], chm[kDmaB];
 #pragma unroll
     for (int i = 0; i < kDmaA; ++i) {
         const int row = (wave * kDmaA + i) * 8 + (lane >> 3);
-        chw[i] = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
-        okw[i] = j0 + row < a.d;
-        offw[i] = okw[i] ? static_cast<uint32_t>(j0 + row) * row_bytes + chw[i] : 0u;
+        const uint32_t ch = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
+        offw[i] = j0 + row < a.d ? static_cast<uint32_t>(j0 + row) * row_bytes + ch : a.w_bytes;
     }
 #pragma unroll
     for (int i = 0; i < kDmaB; ++i) {
         const int row = (wave * kDmaB + i) * 8 + (lane >> 3);
-        chm[i] = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
-        okm[i] = n0 + row < a.n;
-        offm[i] = okm[i] ? static_cast<uint32_t>(n0 + row) * row_bytes + chm[i] : 0u;
+        const uint32_t ch = static_cast<uint32_t>((lane & 7) ^ ((row >> 1) & 7)) * 16u;
+        offm[i] = n0 + row < a.n ? static_cast<uint32_t>(n0 + row) * row_bytes + ch : a.mem_bytes;
     }
     const uint32_t ring_lds = lds_addr(ring);
     auto issue_a = [&](int sl, int i) {
-        const uint32_t kb = static_cast<uint32_t>(sl) * kSlab;
         const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl) % kUnits) * kUnit +
-                             static_cast<uint32_t>(wave * kDmaA + i) * 1024u;
-        dma16(rsrc_w, __builtin_amdgcn_readfirstlane(dst), okw[i] && kb + chw[i] < row_bytes ? offw[i] + kb : a.w_bytes);
+                             (wave_s * kDmaA + static_cast<uint32_t>(i)) * 1024u;
+        dma16_so(rsrc_w, __builtin_amdgcn_readfirstlane(dst), offw[i], static_cast<uint32_t>(sl) * kSlab);
     };
     auto issue_b = [&](int sl, int i) {
-        const uint32_t kb = static_cast<uint32_t>(sl) * kSlab;
         const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl + 1) % kUnits) * kUnit +
-                             static_cast<uint32_t>(wave * kDmaB + i) * 1024u;
-        dma16(rsrc_m, __builtin_amdgcn_readfirstlane(dst), okm[i] && kb + chm[i] < row_bytes ? offm[i] + kb : a.mem_bytes);
+                             (wave_s * kDmaB + static_cast<uint32_t>(i)) * 1024u;
+        dma16_so(rsrc_m, __builtin_amdgcn_readfirstlane(dst), offm[i], static_cast<uint32_t>(sl) * kSlab);
     };
     auto unit_a = [&](int sl) { return ring + ((2 * sl) % kUnits) * kUnit; };
     auto unit_b = [&](int sl) { return ring + ((2 * sl + 1) % kUnits) * kUnit; };
@@ -1218,8 +1228,8 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
         return check_launch("me_gate_residual (value pass)");                                   \
     } while (0)
     if (dtype == ME_BF16) {
-        if (hidden_dtype == ME_BF16 && prefetch) {
-            // 256 x 224 tiles (16x16x32 MFMAs)
+        if (hidden_dtype == ME_BF16 && prefetch && (mem_dim * 2) % kSlab == 0 && mem_dim * 2 >= 3 * kSlab) {
+            // 256 x 224 tiles (16x16x32 MFMAs): whole slabs, at least three
             ak.n_jt = av.n_jt = static_cast<int>(ceil_div(model_dim, kTJ));
             ak.total_tiles = av.total_tiles = ak.n_jt * ak.n_nt;
             ak.per_xcd = av.per_xcd = static_cast<int>(ceil_div(ak.total_tiles, kXcds));
