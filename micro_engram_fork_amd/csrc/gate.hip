@@ -732,8 +732,6 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wj = wave >> 1, wn = wave & 1;
 
-    float alpha_reg = 0.f;
-    if (PHASE == kValue && n0 + tid < a.n) alpha_reg = a.alpha_eff[n0 + tid];
 
     // ---- epilogue row walk geometry: 14 of 16 lanes x 16 bytes per token row (the wave's 112
     // columns), lane l16 owning 8 columns, rows rsub, rsub + 4, ... of the wave's 128 tokens
@@ -827,7 +825,36 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
 #pragma unroll
         for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
     }
-    wait_vmcnt<kDmaA + kDmaB>();  // A_0, B_0 landed (A_1, B_1 may fly)
+    // value pass: the gate of token n0 + tid from the key pass's partial sums, summed in column
+    // tile order exactly as gate_alpha_kernel sums them, while the first slabs land (the tiles
+    // of column tile 0 also write the gates and row stats the caller asked for)
+    float alpha_reg = 0.f;
+    if (PHASE == kValue && n0 + tid < a.n) {
+        const int64_t n = n0 + tid;
+        float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+#pragma unroll 8
+        for (int t = 0; t < a.n_jt; ++t) {
+            const float *p = a.partials + (static_cast<int64_t>(t) * a.n + n) * 3;
+            sk2 += p[0];
+            sck += p[1];
+            sx2 += p[2];
+        }
+        float alpha = gate_alpha(sx2, sk2, sck, a);
+        if (jt == 0) {
+            if (a.alpha_out != nullptr) a.alpha_out[n] = alpha;
+            if (a.row_stats_out != nullptr) {
+                float *st = a.row_stats_out + n * 4;
+                st[0] = sx2;
+                st[1] = sk2;
+                st[2] = sck;
+                st[3] = alpha;
+            }
+        }
+        if (a.keep != nullptr && a.keep[n] == 0) alpha = 0.f;
+        alpha_reg = alpha;
+    }
+    wait_vmcnt<kDmaA + kDmaB>();  // A_0, B_0 landed (A_1, B_1 may fly; loads issued after them only
+                                  // make this wait longer)
     __syncthreads();
     Frag16 f0, f1;
     // fragment parts in the order the next k-step's MFMAs use them: a0, b0..b7, a1..a6
@@ -1235,12 +1262,9 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
             ak.per_xcd = av.per_xcd = static_cast<int>(ceil_div(ak.total_tiles, kXcds));
             const dim3 grid16(static_cast<unsigned>(ak.per_xcd * kXcds));
             hipLaunchKernelGGL(gate224_kernel<kKey>, grid16, dim3(kThreads), 0, s, ak);
-            int st_ = check_launch("me_gate_residual (key pass)");
+            const int st_ = check_launch("me_gate_residual (key pass)");
             if (st_ != ME_OK) return st_;
-            hipLaunchKernelGGL(gate_alpha_kernel, dim3(static_cast<unsigned>(ceil_div(n, kThreads))),
-                               dim3(kThreads), 0, s, ak);
-            st_ = check_launch("me_gate_residual (gate)");
-            if (st_ != ME_OK) return st_;
+            // the value pass computes each token's gate itself (no gate_alpha_kernel launch)
             hipLaunchKernelGGL(gate224_kernel<kValue>, grid16, dim3(kThreads), 0, s, av);
             return check_launch("me_gate_residual (value pass)");
         }

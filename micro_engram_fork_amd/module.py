@@ -366,10 +366,11 @@ class MicroEngram(nn.Module):
 
     # Token counts up to which the gate without gradients runs the two projections as one
     # library GEMM against the stacked [W_K; W_V] plus the row kernel (me_gate_rows) instead of
-    # the fused kernel's 256 x 256 tiles, which leave CUs idle below a few thousand tokens
-    # (measured on MI355X, model dim 5376, memory dim 1536: 256 tokens ~25 us against ~90 us,
-    # 4096 tokens ~145 us against ~199 us; at 8192 the two are even).
-    few_tokens_max = 4096
+    # the fused kernel, whose 256-token tiles come in whole rounds of the CUs and leave many of
+    # them idle below the last round (measured on MI355X, model dim 5376, memory dim 1536:
+    # 512 tokens ~30 us against ~83 us, 4096 ~147 against ~186, 6144 ~227 against ~278; at
+    # 8192 the fused kernel is ahead, ~299 against ~305).
+    few_tokens_max = 6144
 
     def _kv_weight(self):
         """[W_K; W_V] ([2d, M]) stacked once and kept while neither weight changes (same
