@@ -134,7 +134,8 @@ int me_hash_prev_gather(const void *ids, int ids_dtype, int64_t n, int64_t width
 
 /*
  * me_gate_workspace_size -- bytes of workspace me_gate_residual needs for n tokens of
- * model_dim (per-token partial sums of the gate, one triple per 256-column tile).
+ * model_dim (per-token partial sums of the gate, one triple per column tile of 224, the
+ * narrower of the two tilings, and the per-token gates).
  */
 int me_gate_workspace_size(int64_t n, int64_t model_dim, size_t *bytes);
 
@@ -170,7 +171,7 @@ int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n, int64_t mo
 /*
  * me_gate_rows -- the gate and residual add of me_gate_residual from key and value projections
  * computed elsewhere (few-token batches, where one GEMM of the memory vectors against the
- * stacked [W_K; W_V] on the library BLAS fills the part and me_gate_residual's 256 x 256 tiles
+ * stacked [W_K; W_V] on the library BLAS fills the part and me_gate_residual's 256-token tiles
  * would not). Replaces the rest of MicroEngram.inject after the two nn.Linear calls
  * (micro_engram/module.py:240-261), with the same arithmetic as me_gate_residual:
  *
