@@ -7,9 +7,9 @@
 //   s = sum(h * k) / sqrt(d); scalar_sqrt: s = sign(s) * sqrt(max(|s|, 1e-6))
 //   alpha = sigmoid(s); out = x + round_H(alpha * V * keep)
 //
-// The fused two-pass kernel (gate.hip) computes K and V tile by tile on 256 x 256 MFMA tiles:
+// The fused two-pass kernel (gate.hip) computes K and V tile by tile on 256-token MFMA tiles:
 // below a few thousand tokens it has fewer tiles than the part has CUs, and one tile's K loop
-// sets its time (a 256-token decode batch: ~90 us). For such batches the projections run as
+// sets its time (a 512-token batch: ~83 us). For such batches the projections run as
 // one plain GEMM of the memory vectors against the stacked [W_K; W_V] (the library BLAS
 // spreads small M over every CU), and this kernel does the rest in one pass over the rows:
 // one 256-thread workgroup per token (a decode batch of 256 tokens fills the part's 256 CUs),
