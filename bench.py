@@ -25,6 +25,10 @@ all inputs already in HBM. Prints one JSON line:
   roofline_update  the training-side sparse update of a batch of this shape (dedup of the
                 196,608 lookups + row-wise Adam with stochastic rounding on the touched rows),
                 algorithmic bytes / duration (graph replay) over 16 distinct batches
+  training_step  one training step of a second engram of the same shape with row-sharded
+                tables (sparse row gradients): forward with gradients, backward from a fixed
+                output gradient, clip (a host read, as the reference's trainer does) and the
+                row tables' lazy row-wise Adam step; wall clock over synchronised steps
   cpu_baseline  the oracle's torch-CPU forward on a token sample of the same batch
 """
 import argparse
@@ -36,7 +40,7 @@ import time
 import numpy as np
 import torch
 
-from micro_engram_fork_amd import ops, synthetic
+from micro_engram_fork_amd import ops, rows, synthetic
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -100,6 +104,42 @@ def update_bytes(n_lookups, n_uniq, dim, esize):
     dedup = n_lookups * (8 + 4 * dim) + n_uniq * (8 + 4 * dim) + n_lookups * 8
     adam = n_uniq * (4 * dim * esize + 8 + 4 * dim + 8)
     return dedup, adam
+
+
+def training_step_ms(dev, batches, steps, warmup):
+    """Mean wall-clock ms of one training step on a second engram of the workload's shape with
+    row-sharded tables: forward with gradients (hash, differentiable row lookup, gate), backward
+    from a fixed output gradient (gate backward, weight GEMMs, dedup of the row gradients), the
+    tables' gradient norm (clip, a host read) and the lazy row-wise Adam step with stochastic
+    rounding. The dense weights' gradients are dropped each step (their optimizer is not on the
+    lookup path)."""
+    eng = synthetic.build_engram("gemma", dev, seed=1)
+    eng.shard_rows(0, 1, device=dev)
+    rt = rows.RowTables([("model.layers.0.micro_engram.", eng)], lr=5e-3, lazy=True, rowwise=True,
+                        sparse_grads=True, seed=2024)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    gout = torch.randn(batches[0][2].shape, generator=gen, device=dev).to(torch.bfloat16) * 1e-3
+
+    def step(k):
+        ids, pos, hidden = batches[k % CYCLE]
+        h = hidden.detach().requires_grad_(True)
+        eng(h, ids, pos).backward(gout)
+        rt.clip(1.0)
+        rt.step(5e-3)
+        for p in (eng.key.weight, eng.value.weight, eng.q_scale, eng.k_scale):
+            p.grad = None
+
+    for k in range(warmup):
+        step(k)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(warmup + k)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    del rt, eng
+    torch.cuda.empty_cache()
+    return ms
 
 
 def cpu_baseline(eng, ids, pos, hidden, target_s):
@@ -273,6 +313,8 @@ def main():
         n_lookups = ubatches[0][0].numel()
         n_uniq = float(np.mean([u[4] for u in ubatches]))
         del ubatches, exp_avgs, exp_avg_sqs
+    train_ms = training_step_ms(dev, batches, steps=10, warmup=3)
+    with torch.inference_mode():
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         copy_ms = replay_ms([lambda: dst.copy_(src)], 5)
@@ -349,6 +391,12 @@ def main():
             "dedup_gbs": dedup_b / (dedup_ms * 1e-3) / 1e9,
             "adam_ms": adam_ms,
             "adam_gbs": adam_b / (adam_ms * 1e-3) / 1e9,
+        },
+        "training_step": {
+            "workload": "a second engram of the same shape, row-sharded tables: forward with "
+                        "gradients + backward + clip + lazy row-wise Adam (SR) on 8192 tokens",
+            "ms_per_step": train_ms,
+            "tokens_per_s": T / (train_ms * 1e-3),
         },
         "serving_decode": {
             "workload": "the same engram, 256 sequences x 1 token (0-3 history tokens, [256, 4] "

@@ -88,7 +88,14 @@ class _RowLookup(torch.autograd.Function):
             a, b = bounds[k], bounds[k + 1]
             local = uniq[a:b] - ctx.offsets[k]
             if ctx.shards is not None and getattr(ctx.shards[k], "_sparse_rows", False):
-                add_sparse_grad(ctx.shards[k], local, gsum[a:b])
+                shard = ctx.shards[k]
+                if getattr(shard, "sparse_grad", None) is None:
+                    # this table's part of the dedup is already coalesced: unique rows in
+                    # ascending order and fp32 sums that start from +0.0, as index_add_'s do
+                    # (what add_sparse_grad would return for it, without a second dedup)
+                    shard.sparse_grad = (local, gsum[a:b])
+                else:
+                    add_sparse_grad(shard, local, gsum[a:b])
                 grads.append(None)
                 continue
             g = torch.zeros(shape, dtype=torch.float32, device=grad.device)

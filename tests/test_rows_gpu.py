@@ -250,6 +250,32 @@ def test_bf16_stochastic_rounding_tracks_fp32():
     assert abs(moved["sr"] / moved["fp32"] - 1) < 0.03
 
 
+def test_row_lookup_two_backwards_accumulate():
+    # gradient accumulation: each backward sums its own duplicate lookups first (rows.py:117-118),
+    # the first leaves each table's part as its sparse gradient and the second merges its part
+    # into it like add_sparse_grad (rows.py:125-129, 137-147)
+    eng = MicroEngram(model_dim=16, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3),
+                      vocab_size=500, seed=4)
+    shards = eng.shard_rows(0, 1, device=DEV)
+    for s in shards:
+        s._sparse_rows = True
+    passes = []
+    for _ in range(2):
+        ids = torch.randint(0, 500, (2, 40), device=DEV)
+        idx = eng.hash_ids(ids)
+        out = me_rows.row_lookup(eng, idx)
+        grads = [torch.randn_like(o) for o in out]
+        torch.autograd.backward(out, grads)
+        passes.append((idx, grads))
+    for k, s in enumerate(shards):
+        (i1, g1), (i2, g2) = passes[0], passes[1]
+        u1, _, a1 = oracle.dedup(i1[k].reshape(-1).cpu().numpy(), g1[k].reshape(-1, 8).cpu().numpy())
+        u2, _, a2 = oracle.dedup(i2[k].reshape(-1).cpu().numpy(), g2[k].reshape(-1, 8).cpu().numpy())
+        u, _, acc = oracle.dedup(np.concatenate([u1, u2]), np.concatenate([a1, a2]))
+        assert np.array_equal(s.sparse_grad[0].cpu().numpy(), u)
+        assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
 def test_row_lookup_backward_sparse_grads():
     eng = MicroEngram(model_dim=16, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3),
                       vocab_size=500, seed=3)
