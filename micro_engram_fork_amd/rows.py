@@ -47,6 +47,23 @@ def add_sparse_grad(p, rows, g):
     p.sparse_grad = (u, acc)
 
 
+def _spans(tensors):
+    """The tensors as few 1-D fp32 views: consecutive contiguous fp32 tensors that tile one
+    buffer in order (the row lookup's backward leaves every table's sparse gradient as the next
+    slice of one dedup output) merge into one view, so one reduction launch covers them."""
+    spans = []
+    for t in tensors:
+        if t.dtype == torch.float32 and t.is_contiguous() and spans:
+            last = spans[-1]
+            if (last.dtype == torch.float32 and
+                    last.untyped_storage().data_ptr() == t.untyped_storage().data_ptr() and
+                    last.data_ptr() + last.numel() * 4 == t.data_ptr()):
+                spans[-1] = last.as_strided((last.numel() + t.numel(),), (1,), last.storage_offset())
+                continue
+        spans.append(t.reshape(-1) if t.is_contiguous() else t)
+    return spans
+
+
 def _table_offsets(engram):
     offs = [0]
     for rows in engram.table_rows:
@@ -80,13 +97,15 @@ class _RowLookup(torch.autograd.Function):
         keys = (idx2d + offs[:, None]).t().reshape(-1)
         uniq, _, gsum = dedup_rows(keys, ctx.offsets[-1], grad.reshape(n * nt, D))
         bounds = torch.searchsorted(uniq, torch.tensor(ctx.offsets, device=uniq.device)).tolist()
+        # every unique key's row in its own table, in a few launches for all tables
+        local_all = uniq - offs[torch.searchsorted(offs, uniq, right=True) - 1]
         grads = []
         for k, (shape, dtype) in enumerate(ctx.shapes):
             if not ctx.needs_input_grad[2 + k]:
                 grads.append(None)
                 continue
             a, b = bounds[k], bounds[k + 1]
-            local = uniq[a:b] - ctx.offsets[k]
+            local = local_all[a:b]
             if ctx.shards is not None and getattr(ctx.shards[k], "_sparse_rows", False):
                 shard = ctx.shards[k]
                 if getattr(shard, "sparse_grad", None) is None:
@@ -148,12 +167,15 @@ class RowTables:
         if not ps:
             return None
         sq = torch.zeros(1, dtype=torch.float32, device=ps[0].device)
+        parts = []
         for p in ps:
             if p.grad is not None:
-                ops.sumsq(p.grad, sq, accumulate=True)
+                parts.append(p.grad)
             sg = getattr(p, "sparse_grad", None)
             if sg is not None:
-                ops.sumsq(sg[1], sq, accumulate=True)
+                parts.append(sg[1])
+        for span in _spans(parts):
+            ops.sumsq(span, sq, accumulate=True)
         if max_norm and max_norm > 0 and self.optimizer is not None:
             self.optimizer.clip_next_step(sq, max_norm)
         self.last_grad_norm = float(sq.sqrt().item())

@@ -1,0 +1,23 @@
+"""Host-side logic of the row tables (CPU): the norm spans of RowTables.clip."""
+import torch
+
+from micro_engram_fork_amd.rows import _spans
+
+
+def test_spans_merge_adjacent_slices_only():
+    # slices that tile one buffer in order become one view; anything else stays apart, and the
+    # squared sum over the spans is the squared sum over the parts
+    buf = torch.arange(40, dtype=torch.float32).reshape(20, 2)
+    other = torch.ones(4, 2)
+    parts = [buf[0:3], buf[3:7], buf[7:20], other, buf[0:2], buf[5:8]]
+    spans = _spans(parts)
+    assert [s.numel() for s in spans] == [40, 8, 4, 6]
+    assert spans[0].data_ptr() == buf.data_ptr() and spans[0].dim() == 1
+    assert torch.equal(spans[0], buf.reshape(-1))
+    assert float(sum(s.pow(2).sum() for s in spans)) == float(sum(p.pow(2).sum() for p in parts))
+
+
+def test_spans_keep_other_dtypes_and_gaps_apart():
+    buf = torch.zeros(10, dtype=torch.float32)
+    parts = [buf[0:4], buf[5:9], torch.zeros(3, dtype=torch.bfloat16)]
+    assert [s.numel() for s in _spans(parts)] == [4, 4, 3]
