@@ -884,7 +884,11 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        constexpr int kPre = 8;  // MFMAs of k-step 1 before the wait and the barrier
+        constexpr int kPre = 16;  // MFMAs of k-step 1 before the wait and the barrier
+        // every fragment read of the next k-step has an MFMA slot: k-step 0 reads after every
+        // third MFMA, k-step 1 after every second one past the barrier (B loads first)
+        static_assert(3 * kParts <= kMfma && kPre + 2 * kParts <= kMfma && kDmaB <= kMfma - kPre,
+                      "fragment reads and loads fit the k-steps' MFMAs");
 #pragma unroll
         for (int i = 0; i < kPre; ++i) {
             acc[i / kSubN][i % kSubN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
