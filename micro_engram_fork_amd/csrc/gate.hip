@@ -64,6 +64,7 @@ constexpr int kWaveStage = 128 * kStagePitch;      // one wave's staged 128-row 
 constexpr int kGroupTiles = 8;                     // token tiles per XCD group
 constexpr int kXcds = 8;
 constexpr uint32_t kBufferConfig = 0x00020000u;    // raw buffer descriptor word 3 (gfx9 family)
+constexpr int kStoreNT = 2;                        // buffer store cache policy bit: non-temporal
 static_assert(4 * kWaveStage + 2 * kTile * 3 * 4 <= kRingBytes, "epilogue must fit in the ring");
 
 // Forward passes (key, value) and the backward's two passes over the same GEMM tiles.
@@ -116,6 +117,17 @@ __device__ __forceinline__ uint16_t from_f<uint16_t>(float v) { return float_to_
 // Rounding of a value to storage type T, kept as float.
 template <typename T>
 __device__ __forceinline__ float round_t(float v) { return to_f<T>(from_f<T>(v)); }
+
+// Two floats rounded to bf16 (nearest, ties to even) in one word, `lo` in the low half: one
+// v_cvt_pk_bf16_f32 for the pair.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3_v __attribute__((ext_vector_type(3)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){lo, hi}, bf16x2_t));
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // E consecutive elements of X (E * sizeof(X) a multiple of 8 bytes, 8-byte aligned) as floats.
 template <typename X, int E>
@@ -747,13 +759,21 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     u32x4_v spre[PHASE == kKey ? 4 : 1];
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+    // byte offset of the lane's 16 bytes in its row u (token ntok0 + 4u + rsub) of hidden and of
+    // the output (same layout): the lane's first row plus u row strides, or the range end (reads
+    // zeros, stores nothing) for a row past n or a lane past d; hidden is under 2 GiB
+    const int rows_left = jok ? static_cast<int>(max(min(a.n - (ntok0 + rsub), static_cast<int64_t>(kTile)),
+                                                     static_cast<int64_t>(0)))
+                              : 0;
+    const uint32_t xoff0 = jok ? static_cast<uint32_t>(((ntok0 + rsub) * a.d + jl) * 2) : 0u;
+    const uint32_t xstride = static_cast<uint32_t>(a.d * 8);  // four rows
+    auto row_off = [&](int u) { return 4 * u < rows_left ? xoff0 + static_cast<uint32_t>(u) * xstride : a.hidden_bytes; };
+    const __amdgpu_buffer_rsrc_t ro =
+        __builtin_amdgcn_make_buffer_rsrc(a.out, 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
     auto load_rows = [&](int u0, int u1) {
 #pragma unroll
-        for (int u = u0; u < u1; ++u) {
-            const int64_t n = ntok0 + u * 4 + rsub;
-            const uint32_t off = jok && n < a.n ? static_cast<uint32_t>((n * a.d + jl) * 2) : a.hidden_bytes;
-            xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0));
-        }
+        for (int u = u0; u < u1; ++u)
+            xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, row_off(u), 0, 0));
     };
     auto prefetch = [&]() {
         load_rows(0, kPfRows);
@@ -818,40 +838,95 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[x][y][e] = 0.f;
 
+    auto issue_first_slabs = [&]() {
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
+        for (int sl = 0; sl < 2; ++sl) {
 #pragma unroll
-        for (int i = 0; i < kDmaA; ++i) issue_a(sl, i);
+            for (int i = 0; i < kDmaA; ++i) issue_a(sl, i);
 #pragma unroll
-        for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
-    }
+            for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
+        }
+    };
     // value pass: the gate of token n0 + tid from the key pass's partial sums, summed in column
     // tile order exactly as gate_alpha_kernel sums them, while the first slabs land (the tiles
-    // of column tile 0 also write the gates and row stats the caller asked for)
+    // of column tile 0 also write the gates and row stats the caller asked for). Up to kMaxJt
+    // column tiles the sums are loaded first and the first two slabs' rows after them through
+    // the compiler's buffer-to-LDS builtin, which the compiler counts: waiting for the sums then
+    // leaves the rows in flight (loads complete in issue order). Past kMaxJt the sums are read
+    // after the rows are issued.
     float alpha_reg = 0.f;
-    if (PHASE == kValue && n0 + tid < a.n) {
-        const int64_t n = n0 + tid;
-        float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
-#pragma unroll 8
-        for (int t = 0; t < a.n_jt; ++t) {
-            const float *p = a.partials + (static_cast<int64_t>(t) * a.n + n) * 3;
-            sk2 += p[0];
-            sck += p[1];
-            sx2 += p[2];
-        }
+    const int64_t n_tok = n0 + tid;
+    auto set_alpha = [&](float sk2, float sck, float sx2) {
         float alpha = gate_alpha(sx2, sk2, sck, a);
         if (jt == 0) {
-            if (a.alpha_out != nullptr) a.alpha_out[n] = alpha;
+            if (a.alpha_out != nullptr) a.alpha_out[n_tok] = alpha;
             if (a.row_stats_out != nullptr) {
-                float *st = a.row_stats_out + n * 4;
+                float *st = a.row_stats_out + n_tok * 4;
                 st[0] = sx2;
                 st[1] = sk2;
                 st[2] = sck;
                 st[3] = alpha;
             }
         }
-        if (a.keep != nullptr && a.keep[n] == 0) alpha = 0.f;
+        if (a.keep != nullptr && a.keep[n_tok] == 0) alpha = 0.f;
         alpha_reg = alpha;
+    };
+    constexpr int kMaxJt = 32;
+    if (PHASE == kValue && a.n_jt <= kMaxJt) {
+        // the partials are [n_jt][n][3] floats, under 2^31 bytes here (n * d < 2^30)
+        const uint32_t pbytes = static_cast<uint32_t>(a.n_jt * a.n * 12);
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc(a.partials, 0, static_cast<int>(pbytes), kBufferConfig);
+        const uint32_t pv = n_tok < a.n ? static_cast<uint32_t>(n_tok * 12) : pbytes;
+        u32x3_v part[kMaxJt];
+#pragma unroll
+        for (int t = 0; t < kMaxJt; ++t)
+            if (t < a.n_jt)
+                part[t] = __builtin_amdgcn_raw_buffer_load_b96(rp, pv, static_cast<uint32_t>(t * a.n * 12), 0);
+        __builtin_amdgcn_sched_barrier(0);
+        const __amdgpu_buffer_rsrc_t rw =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, static_cast<int>(a.w_bytes), kBufferConfig);
+        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(a.mem), 0, static_cast<int>(a.mem_bytes), kBufferConfig);
+        auto *ring3 = (__attribute__((address_space(3))) uint8_t *)(ring);
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+            for (int i = 0; i < kDmaA; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rw, ring3 + (2 * sl) % kUnits * kUnit + (wave_s * kDmaA + i) * 1024u, 16, offw[i],
+                    static_cast<uint32_t>(sl) * kSlab, 0, 0);
+#pragma unroll
+            for (int i = 0; i < kDmaB; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rm, ring3 + (2 * sl + 1) % kUnits * kUnit + (wave_s * kDmaB + i) * 1024u, 16, offm[i],
+                    static_cast<uint32_t>(sl) * kSlab, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (n_tok < a.n) {
+            float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+#pragma unroll
+            for (int t = 0; t < kMaxJt; ++t)
+                if (t < a.n_jt) {
+                    sk2 += __uint_as_float(part[t][0]);
+                    sck += __uint_as_float(part[t][1]);
+                    sx2 += __uint_as_float(part[t][2]);
+                }
+            set_alpha(sk2, sck, sx2);
+        }
+    } else {
+        issue_first_slabs();
+        if (PHASE == kValue && n_tok < a.n) {
+            float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+#pragma unroll 8
+            for (int t = 0; t < a.n_jt; ++t) {
+                const float *p = a.partials + (static_cast<int64_t>(t) * a.n + n_tok) * 3;
+                sk2 += p[0];
+                sck += p[1];
+                sx2 += p[2];
+            }
+            set_alpha(sk2, sck, sx2);
+        }
     }
     wait_vmcnt<kDmaA + kDmaB>();  // A_0, B_0 landed (A_1, B_1 may fly; loads issued after them only
                                   // make this wait longer)
@@ -866,8 +941,12 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     const int pf_at = max(slabs - 3, 0);
     static_assert(kPfLoads + kDmaA + kDmaB <= 63, "vmcnt counts up to 63");
     // Slab s: k-step 0 issues A_{s+2} (into B_{s-1}'s unit, free since the previous barrier) and
-    // reads k-step 1's fragments; k-step 1 waits for slab s+1 after its first 8 MFMAs, passes
+    // reads k-step 1's fragments; k-step 1 waits for slab s+1 after its first kPre MFMAs, passes
     // the barrier, then issues B_{s+2} (into A_s's unit) and reads slab s+1's first fragments.
+    // The row loads go one per kSpreadA (kSpreadB) MFMAs: the four waves leave the barrier
+    // together, and back-to-back loads from all of them queue up behind each other and hold
+    // the MFMAs between them (measured: 281 -> 273 us for the two passes on the Gemma-scale shape).
+    constexpr int kSpreadA = 7, kSpreadB = 4;
     auto slab = [&](int sl, auto wait, auto dma) {
         const uint8_t *ua = unit_a(sl), *ub = unit_b(sl);
 #pragma unroll
@@ -875,8 +954,8 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
             acc[i / kSubN][i % kSubN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                 f0.a[i / kSubN], f0.b[i % kSubN], acc[i / kSubN][i % kSubN], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (decltype(dma)::value && i < kDmaA) {
-                issue_a(sl + 2, i);
+            if (decltype(dma)::value && i % kSpreadA == 0 && i / kSpreadA < kDmaA) {
+                issue_a(sl + 2, i / kSpreadA);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (i % 3 == 2 && i / 3 < kParts) {
@@ -887,7 +966,8 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
         constexpr int kPre = 16;  // MFMAs of k-step 1 before the wait and the barrier
         // every fragment read of the next k-step has an MFMA slot: k-step 0 reads after every
         // third MFMA, k-step 1 after every second one past the barrier (B loads first)
-        static_assert(3 * kParts <= kMfma && kPre + 2 * kParts <= kMfma && kDmaB <= kMfma - kPre,
+        static_assert(3 * kParts <= kMfma && kPre + 2 * kParts <= kMfma &&
+                          kSpreadA * (kDmaA - 1) < kMfma && kSpreadB * (kDmaB - 1) < kMfma - kPre,
                       "fragment reads and loads fit the k-steps' MFMAs");
 #pragma unroll
         for (int i = 0; i < kPre; ++i) {
@@ -908,8 +988,8 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
                 f1.a[i / kSubN], f1.b[i % kSubN], acc[i / kSubN][i % kSubN], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             const int q = i - kPre;
-            if (decltype(dma)::value && q < kDmaB) {
-                issue_b(sl + 2, q);
+            if (decltype(dma)::value && q % kSpreadB == 0 && q / kSpreadB < kDmaB) {
+                issue_b(sl + 2, q / kSpreadB);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (q % 2 == 1 && q / 2 < kParts) {  // past the last slab these read a stale unit; unused
@@ -980,9 +1060,10 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
 #pragma unroll
     for (int u = 0; u < 32; ++u) {
         const int row = u * 4 + rsub;
-        const int64_t n = ntok0 + row;
         uint32_t cw[4] = {0u, 0u, 0u, 0u};
-        if (l16 < kWJ / kLaneCols) {
+        // lanes 14 and 15 of a row hold no columns: in the value pass they read the pad and the
+        // next row (or the gates past the last row; all inside the ring) and store nothing
+        if (PHASE == kValue || l16 < kWJ / kLaneCols) {
             const uint8_t *sp = stage + row * kPitch16 + l16 * 16;
             const uint2 c0 = reinterpret_cast<const uint2 *>(sp)[0];
             const uint2 c1 = reinterpret_cast<const uint2 *>(sp)[1];
@@ -1012,17 +1093,16 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
                 p[2] = sx2;
             }
         } else {
-            if (jok && n < a.n) {
-                const float alpha = s_aux[wn * 128 + row];
-                uint32_t ow[4];
-                H *ov = reinterpret_cast<H *>(ow);
+            // x + round(alpha * V), V already rounded, two columns per conversion; a row past n
+            // or a lane past d stores nothing (its offset is the range end)
+            const float alpha = s_aux[wn * 128 + row];
+            u32x4_v o;
 #pragma unroll
-                for (int e = 0; e < kLaneCols; ++e)
-                    ov[e] = from_f<H>(to_f<H>(xv[e]) + round_t<H>(alpha * to_f<T>(cv[e])));
-                uint8_t *p = a.out + (n * a.d + jl) * static_cast<int64_t>(sizeof(H));
-                __builtin_nontemporal_store(u32x2_t{ow[0], ow[1]}, reinterpret_cast<u32x2_t *>(p));
-                __builtin_nontemporal_store(u32x2_t{ow[2], ow[3]}, reinterpret_cast<u32x2_t *>(p) + 1);
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t av = pack_bf16(alpha * bf16_lo(cw[h]), alpha * bf16_hi(cw[h]));
+                o[h] = pack_bf16(bf16_lo(xw[h]) + bf16_lo(av), bf16_hi(xw[h]) + bf16_hi(av));
             }
+            __builtin_amdgcn_raw_buffer_store_b128(o, ro, row_off(u), 0, kStoreNT);
         }
     }
     if constexpr (PHASE == kKey) {
