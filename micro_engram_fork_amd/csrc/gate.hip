@@ -677,9 +677,11 @@ __global__ __launch_bounds__(kThreads, 1) void gate_kernel(const GateArgs a) {
 // 7 x 8 tiles of v_mfma_f32_16x16x32_bf16 (224 accumulators); a slab is two 32-wide k-steps. A
 // slab's 224 W rows take 7 row loads per wave, its 256 mem rows 8. The ring, the swizzle, the
 // load/barrier order and the epilogue follow gate_kernel. Under the last three slabs the
-// workgroup also loads the first 16 of each lane's 32 hidden rows (and the key pass's scale
-// deltas) into registers, so their latency and the HBM burst of every CU reaching its epilogue
-// at once overlap the MFMAs; the other 16 rows are loaded as the K loop ends.
+// workgroup also loads the first of each lane's 32 hidden rows into registers (16 with the key
+// pass's scale deltas; 8 with the key pass's partial sums of the value pass's tokens, from which
+// the value pass computes its gates after the K loop), so their latency and the HBM burst of
+// every CU reaching its epilogue at once overlap the MFMAs; the other rows are loaded as the K
+// loop ends.
 constexpr int kTJ = 224;                // output columns per tile
 constexpr int kWJ = kTJ / 2;            // columns per wave (112)
 constexpr int kSubJ = kWJ / 16;         // 16-row A subtiles per wave (7)
@@ -752,9 +754,34 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     const int64_t ntok0 = n0 + wn * 128;
     const int64_t jl = j0 + wj * kWJ + l16 * kLaneCols;  // lane's first column
     const bool jok = l16 < kWJ / kLaneCols && jl < a.d;  // d is a multiple of 8
-    // hidden rows 0..kPfRows-1 are loaded under the last slabs, the rest at the epilogue start
-    constexpr int kPfRows = 16;
-    constexpr int kPfLoads = kPfRows + (PHASE == kKey ? 4 : 0);
+    // hidden rows 0..kPfRows-1 are loaded under the last slabs, the rest at the epilogue start;
+    // with them the key pass loads its scale deltas and the value pass the key pass's partial
+    // sums of token n0 + tid (kPartLoads column tiles, always that many loads so that the slab
+    // waits count a fixed number; the ones past n_jt read zeros and are not summed)
+    constexpr int kPfRows = PHASE == kKey ? 16 : 8;
+    constexpr int kPartLoads = 24;
+    constexpr int kPfLoads = kPfRows + (PHASE == kKey ? 4 : kPartLoads);
+    const int64_t n_tok = n0 + tid;
+    const bool parts_late = PHASE == kValue && a.n_jt <= kPartLoads;
+    float alpha_reg = 0.f;
+    // the gate of token n_tok, summed in column tile order exactly as gate_alpha_kernel sums
+    // them (the tiles of column tile 0 also write the gates and row stats the caller asked for)
+    auto set_alpha = [&](float sk2, float sck, float sx2) {
+        float alpha = gate_alpha(sx2, sk2, sck, a);
+        if (jt == 0) {
+            if (a.alpha_out != nullptr) a.alpha_out[n_tok] = alpha;
+            if (a.row_stats_out != nullptr) {
+                float *st = a.row_stats_out + n_tok * 4;
+                st[0] = sx2;
+                st[1] = sk2;
+                st[2] = sck;
+                st[3] = alpha;
+            }
+        }
+        if (a.keep != nullptr && a.keep[n_tok] == 0) alpha = 0.f;
+        alpha_reg = alpha;
+    };
+    u32x3_v part[PHASE == kValue ? kPartLoads : 1];
     u32x4_v xpre[32];
     u32x4_v spre[PHASE == kKey ? 4 : 1];
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
@@ -788,6 +815,16 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
             spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
             spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
             spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+        } else {
+            // the partials are [n_jt][n][3] floats (n * d < 2^30 here, so under 2^31 bytes)
+            const uint32_t pbytes = static_cast<uint32_t>(a.n_jt * a.n * 12);
+            const __amdgpu_buffer_rsrc_t rp =
+                __builtin_amdgcn_make_buffer_rsrc(a.partials, 0, static_cast<int>(pbytes), kBufferConfig);
+            const uint32_t pv = parts_late && n_tok < a.n ? static_cast<uint32_t>(n_tok * 12) : pbytes;
+#pragma unroll
+            for (int t = 0; t < kPartLoads; ++t)
+                part[t] = __builtin_amdgcn_raw_buffer_load_b96(rp, t < a.n_jt ? pv : pbytes,
+                                                               static_cast<uint32_t>(t * a.n * 12), 0);
         }
     };
 
@@ -838,95 +875,26 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[x][y][e] = 0.f;
 
-    auto issue_first_slabs = [&]() {
 #pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
+    for (int sl = 0; sl < 2; ++sl) {
 #pragma unroll
-            for (int i = 0; i < kDmaA; ++i) issue_a(sl, i);
+        for (int i = 0; i < kDmaA; ++i) issue_a(sl, i);
 #pragma unroll
-            for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
-        }
-    };
-    // value pass: the gate of token n0 + tid from the key pass's partial sums, summed in column
-    // tile order exactly as gate_alpha_kernel sums them, while the first slabs land (the tiles
-    // of column tile 0 also write the gates and row stats the caller asked for). Up to kMaxJt
-    // column tiles the sums are loaded first and the first two slabs' rows after them through
-    // the compiler's buffer-to-LDS builtin, which the compiler counts: waiting for the sums then
-    // leaves the rows in flight (loads complete in issue order). Past kMaxJt the sums are read
-    // after the rows are issued.
-    float alpha_reg = 0.f;
-    const int64_t n_tok = n0 + tid;
-    auto set_alpha = [&](float sk2, float sck, float sx2) {
-        float alpha = gate_alpha(sx2, sk2, sck, a);
-        if (jt == 0) {
-            if (a.alpha_out != nullptr) a.alpha_out[n_tok] = alpha;
-            if (a.row_stats_out != nullptr) {
-                float *st = a.row_stats_out + n_tok * 4;
-                st[0] = sx2;
-                st[1] = sk2;
-                st[2] = sck;
-                st[3] = alpha;
-            }
-        }
-        if (a.keep != nullptr && a.keep[n_tok] == 0) alpha = 0.f;
-        alpha_reg = alpha;
-    };
-    constexpr int kMaxJt = 32;
-    if (PHASE == kValue && a.n_jt <= kMaxJt) {
-        // the partials are [n_jt][n][3] floats, under 2^31 bytes here (n * d < 2^30)
-        const uint32_t pbytes = static_cast<uint32_t>(a.n_jt * a.n * 12);
-        const __amdgpu_buffer_rsrc_t rp =
-            __builtin_amdgcn_make_buffer_rsrc(a.partials, 0, static_cast<int>(pbytes), kBufferConfig);
-        const uint32_t pv = n_tok < a.n ? static_cast<uint32_t>(n_tok * 12) : pbytes;
-        u32x3_v part[kMaxJt];
-#pragma unroll
-        for (int t = 0; t < kMaxJt; ++t)
-            if (t < a.n_jt)
-                part[t] = __builtin_amdgcn_raw_buffer_load_b96(rp, pv, static_cast<uint32_t>(t * a.n * 12), 0);
-        __builtin_amdgcn_sched_barrier(0);
-        const __amdgpu_buffer_rsrc_t rw =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, static_cast<int>(a.w_bytes), kBufferConfig);
-        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(a.mem), 0, static_cast<int>(a.mem_bytes), kBufferConfig);
-        auto *ring3 = (__attribute__((address_space(3))) uint8_t *)(ring);
-#pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-#pragma unroll
-            for (int i = 0; i < kDmaA; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rw, ring3 + (2 * sl) % kUnits * kUnit + (wave_s * kDmaA + i) * 1024u, 16, offw[i],
-                    static_cast<uint32_t>(sl) * kSlab, 0, 0);
-#pragma unroll
-            for (int i = 0; i < kDmaB; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rm, ring3 + (2 * sl + 1) % kUnits * kUnit + (wave_s * kDmaB + i) * 1024u, 16, offm[i],
-                    static_cast<uint32_t>(sl) * kSlab, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (n_tok < a.n) {
-            float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
-#pragma unroll
-            for (int t = 0; t < kMaxJt; ++t)
-                if (t < a.n_jt) {
-                    sk2 += __uint_as_float(part[t][0]);
-                    sck += __uint_as_float(part[t][1]);
-                    sx2 += __uint_as_float(part[t][2]);
-                }
-            set_alpha(sk2, sck, sx2);
-        }
-    } else {
-        issue_first_slabs();
-        if (PHASE == kValue && n_tok < a.n) {
-            float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+        for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
+    }
+    // value pass, more than kPartLoads column tiles: the gate of token n0 + tid from the key
+    // pass's partial sums while the first slabs land (otherwise the sums are loaded with the
+    // epilogue prefetch and the gate is computed after the K loop)
+    if (PHASE == kValue && !parts_late && n_tok < a.n) {
+        float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
 #pragma unroll 8
-            for (int t = 0; t < a.n_jt; ++t) {
-                const float *p = a.partials + (static_cast<int64_t>(t) * a.n + n_tok) * 3;
-                sk2 += p[0];
-                sck += p[1];
-                sx2 += p[2];
-            }
-            set_alpha(sk2, sck, sx2);
+        for (int t = 0; t < a.n_jt; ++t) {
+            const float *p = a.partials + (static_cast<int64_t>(t) * a.n + n_tok) * 3;
+            sk2 += p[0];
+            sck += p[1];
+            sx2 += p[2];
         }
+        set_alpha(sk2, sck, sx2);
     }
     wait_vmcnt<kDmaA + kDmaB>();  // A_0, B_0 landed (A_1, B_1 may fly; loads issued after them only
                                   // make this wait longer)
@@ -1011,6 +979,17 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
     __syncthreads();  // the ring is free for the epilogue
     load_rows(kPfRows, 32);
+    if (parts_late && n_tok < a.n) {
+        float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+#pragma unroll
+        for (int t = 0; t < kPartLoads; ++t)
+            if (t < a.n_jt) {
+                sk2 += __uint_as_float(part[t][0]);
+                sck += __uint_as_float(part[t][1]);
+                sx2 += __uint_as_float(part[t][2]);
+            }
+        set_alpha(sk2, sck, sx2);
+    }
 
     // ---- epilogue: each wave stages round_T of its 128 x 112 tile as [token][column] rows
     uint8_t *stage = ring + wave * kWaveStage16;
