@@ -855,15 +855,21 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
         offm[i] = n0 + row < a.n ? static_cast<uint32_t>(n0 + row) * row_bytes + ch : a.mem_bytes;
     }
     const uint32_t ring_lds = lds_addr(ring);
+    // LDS destination of a load: the wave's first row in the unit, made opaque on a scalar register
+    // per load so that the compiler adds the load's 1 KiB step there (left alone it keeps fifteen
+    // hoisted destinations in vector registers and moves each back to a scalar: two vector
+    // instructions and a wait state per load)
+    const uint32_t wa0 = __builtin_amdgcn_readfirstlane(ring_lds + wave_s * (kDmaA * 1024u));
+    const uint32_t wb0 = __builtin_amdgcn_readfirstlane(ring_lds + wave_s * (kDmaB * 1024u));
     auto issue_a = [&](int sl, int i) {
-        const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl) % kUnits) * kUnit +
-                             (wave_s * kDmaA + static_cast<uint32_t>(i)) * 1024u;
-        dma16_so(rsrc_w, __builtin_amdgcn_readfirstlane(dst), offw[i], static_cast<uint32_t>(sl) * kSlab);
+        uint32_t dst = wa0 + static_cast<uint32_t>((2 * sl) % kUnits) * kUnit;
+        asm volatile("" : "+s"(dst));
+        dma16_so(rsrc_w, dst + static_cast<uint32_t>(i) * 1024u, offw[i], static_cast<uint32_t>(sl) * kSlab);
     };
     auto issue_b = [&](int sl, int i) {
-        const uint32_t dst = ring_lds + static_cast<uint32_t>((2 * sl + 1) % kUnits) * kUnit +
-                             (wave_s * kDmaB + static_cast<uint32_t>(i)) * 1024u;
-        dma16_so(rsrc_m, __builtin_amdgcn_readfirstlane(dst), offm[i], static_cast<uint32_t>(sl) * kSlab);
+        uint32_t dst = wb0 + static_cast<uint32_t>((2 * sl + 1) % kUnits) * kUnit;
+        asm volatile("" : "+s"(dst));
+        dma16_so(rsrc_m, dst + static_cast<uint32_t>(i) * 1024u, offm[i], static_cast<uint32_t>(sl) * kSlab);
     };
     auto unit_a = [&](int sl) { return ring + ((2 * sl) % kUnits) * kUnit; };
     auto unit_b = [&](int sl) { return ring + ((2 * sl + 1) % kUnits) * kUnit; };
