@@ -174,12 +174,13 @@ def test_golden_inject_fixture():
 
 @pytest.mark.parametrize("n,d,dim,heads", [(300, 264, 8, 3), (513, 1024, 16, 2), (7, 4096, 64, 8),
                                             (600, 776, 64, 8), (1100, 520, 32, 5), (260, 448, 64, 1),
-                                            (50, 232, 32, 2)])
+                                            (50, 232, 32, 2), (40, 5632, 32, 2)])
 def test_ragged_shapes_bf16(n, d, dim, heads):
     # token counts and model dims that are not multiples of the tiles; K from 2 to 24 128-byte
     # slabs. Whole slabs, at least three, take the 224-column kernel (M = 192: three slabs, d = 448
-    # two whole column tiles, d = 232 a second tile of 8 columns); partial slabs the 256 x 256 one
-    # (M = 72, 96, 480)
+    # two whole column tiles, d = 232 a second tile of 8 columns, d = 5632 26 column tiles, past
+    # the 24 whose gate sums the value pass loads late, the last of 32 columns); partial slabs the
+    # 256 x 256 one (M = 72, 96, 480)
     torch.manual_seed(n)
     eng = _make(torch.bfloat16, d=d, dim=dim, heads=heads, orders=(2, 3, 4))
     ids = torch.randint(0, 1000, (1, n), device=DEV)
