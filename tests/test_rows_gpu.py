@@ -96,11 +96,14 @@ def test_add_sparse_grad_merges_like_reference():
     assert np.array_equal(p.sparse_grad[1].cpu().numpy().view(np.int32), a.view(np.int32))
 
 
-def test_sumsq():
-    x = torch.randn(123457, device=DEV)
+@pytest.mark.parametrize("n,skip", [(123457, 0), (5, 0), (12_000_003, 3)])
+def test_sumsq(n, skip):
+    # short, tiny and a clip-sized run starting off a 16-byte boundary; two calls agree bit for bit
+    x = torch.randn(n + skip, device=DEV)[skip:]
     got = float(ops.sumsq(x))
     want = float((x.double() ** 2).sum())
     assert abs(got - want) <= 1e-5 * want
+    assert float(ops.sumsq(x)) == got
 
 
 def test_stochastic_bf16_matches_oracle_noise():
