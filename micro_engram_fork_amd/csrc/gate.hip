@@ -937,7 +937,9 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        constexpr int kPre = 16;  // MFMAs of k-step 1 before the wait and the barrier
+        // MFMAs of k-step 1 before the wait and the barrier (on the Gemma-scale shape 12 and 16
+        // took 3 and 6 us longer for the two passes: the barrier waits less for the slowest wave)
+        constexpr int kPre = 20;
         // every fragment read of the next k-step has an MFMA slot: k-step 0 reads after every
         // third MFMA, k-step 1 after every second one past the barrier (B loads first)
         static_assert(3 * kParts <= kMfma && kPre + 2 * kParts <= kMfma &&
