@@ -418,7 +418,7 @@ class MicroEngram(nn.Module):
         stats = getattr(self, "_gate_stats", None)
         if stats is None or stats.device != a.device:
             stats = torch.zeros(3, device=a.device)
-        self._gate_stats = stats + torch.stack([a.sum(), torch.tensor(float(a.numel()), device=a.device),
+        self._gate_stats = stats + torch.stack([a.sum(), a.new_full((), float(a.numel())),
                                                 (a > 0.99).float().sum()])
 
     def pop_gate_stats(self):

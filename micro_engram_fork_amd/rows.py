@@ -71,6 +71,19 @@ def _table_offsets(engram):
     return offs
 
 
+_OFFSETS_ON = {}
+
+
+def _offsets_on(offsets, device):
+    """The table offsets as an int64 tensor on `device`, made once per (offsets, device): a
+    tensor built from a host list per backward is a host-to-device copy on every step."""
+    key = (tuple(offsets), device)
+    t = _OFFSETS_ON.get(key)
+    if t is None:
+        t = _OFFSETS_ON[key] = torch.tensor(offsets, dtype=torch.int64, device=device)
+    return t
+
+
 class _RowLookup(torch.autograd.Function):
     """Per-table rows for hashed ids, world size 1. Backward: the gradient rows of every lookup
     are deduplicated over (table, row) and added to each shard's sparse gradient (shards marked
@@ -90,13 +103,14 @@ class _RowLookup(torch.autograd.Function):
         (idx2d,) = ctx.saved_tensors
         nt, n = idx2d.shape
         D = ctx.shapes[0][0][1]
-        offs = torch.tensor(ctx.offsets[:-1], dtype=torch.int64, device=idx2d.device)
+        offs_all = _offsets_on(ctx.offsets, idx2d.device)
+        offs = offs_all[:-1]
         # token-major flattening: lookup i*nt + k is (token i, table k), whose gradient row is
         # grad[i, k*D:(k+1)*D]; equal keys share a table, so within a key this is token order,
         # the order of the reference's table-major flattening
         keys = (idx2d + offs[:, None]).t().reshape(-1)
         uniq, _, gsum = dedup_rows(keys, ctx.offsets[-1], grad.reshape(n * nt, D))
-        bounds = torch.searchsorted(uniq, torch.tensor(ctx.offsets, device=uniq.device)).tolist()
+        bounds = torch.searchsorted(uniq, offs_all).tolist()
         # every unique key's row in its own table, in a few launches for all tables
         local_all = uniq - offs[torch.searchsorted(offs, uniq, right=True) - 1]
         grads = []
