@@ -56,7 +56,9 @@ class LazyAdamW(torch.optim.Optimizer):
 
     @staticmethod
     def _as_rows(t, n):
-        return t.view(n, -1) if t.dim() >= 2 else t.view(n, 1)
+        if t.dim() == 2:  # tables: already [rows, D] (a view costs a few us of host time per table)
+            return t
+        return t.view(n, -1) if t.dim() > 2 else t.view(n, 1)
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -97,7 +99,7 @@ class LazyAdamW(torch.optim.Optimizer):
                 b["exp_avgs"].append(M)
                 b["exp_avg_sqs"].append(V)
                 b["rows"].append(rows)
-                b["grads"].append(g.reshape(rows.numel(), -1))
+                b["grads"].append(g if g.dim() == 2 and g.shape[0] == rows.numel() else g.reshape(rows.numel(), -1))
                 b["steps"].append(int(state["step"].item()))
                 b["stream_ids"].append(index[id(p)] % 65536)
             for (_, _, rowwise, lazy, _), b in batches.items():
