@@ -109,8 +109,15 @@ class _RowLookup(torch.autograd.Function):
         # grad[i, k*D:(k+1)*D]; equal keys share a table, so within a key this is token order,
         # the order of the reference's table-major flattening
         keys = (idx2d + offs[:, None]).t().reshape(-1)
-        uniq, _, gsum = dedup_rows(keys, ctx.offsets[-1], grad.reshape(n * nt, D))
-        bounds = torch.searchsorted(uniq, offs_all).tolist()
+        # one host read for the unique count and every table's bounds: keys past the count are
+        # masked to the largest int64, so a search over the whole output stops at the count
+        outs = ops.dedup(keys, int(ctx.offsets[-1]), grad.reshape(n * nt, D))
+        count = outs[2].reshape(1)
+        valid = torch.arange(outs[0].numel(), device=keys.device) < count
+        masked = torch.where(valid, outs[0], torch.iinfo(torch.int64).max)
+        host = torch.cat([count, torch.searchsorted(masked, offs_all)]).tolist()
+        bounds = host[1:]
+        uniq, gsum = outs[0][:host[0]], outs[3][:host[0]]
         # every unique key's row in its own table, in a few launches for all tables
         local_all = uniq - offs[torch.searchsorted(offs, uniq, right=True) - 1]
         grads = []
