@@ -27,9 +27,15 @@ all inputs already in HBM. Prints one JSON line:
                 algorithmic bytes / duration (graph replay) over 16 distinct batches
   training_step  one training step of a second engram of the same shape with row-sharded
                 tables (sparse row gradients): forward with gradients, backward from a fixed
-                output gradient, clip (a host read, as the reference's trainer does) and the
-                row tables' lazy row-wise Adam step; wall clock over synchronised steps
-  cpu_baseline  the oracle's torch-CPU forward on a token sample of the same batch
+                output gradient, clip (a host read, as the reference's trainer does), the row
+                tables' lazy row-wise Adam step and the dense weights' AdamW step; wall clock
+                over synchronised steps
+  tiny_forward  the tiny fp32 forward (orders {2,3}, 16 tables of 65,536 rows, hidden 1024,
+                2048 tokens): tokens/s, gather HBM and projection fp32 MFMA rooflines
+  two_engram_canon  two Gemma-scale engrams with a 15 % canon map, 8 x 8192 tokens, chained:
+                tokens/s and the gather's HBM roofline
+  cpu_baseline  the reference path restated in torch-CPU ops (the oracle) on the same batch:
+                hash on all tokens, lookup + inject on a sample, medians of 5 runs
 """
 import argparse
 import json
@@ -41,9 +47,11 @@ import numpy as np
 import torch
 
 from micro_engram_fork_amd import ops, rows, synthetic
+from micro_engram_fork_amd.optim import LazyAdamW
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 
 
 def parse():
@@ -110,13 +118,15 @@ def training_step_ms(dev, batches, steps, warmup):
     """Mean wall-clock ms of one training step on a second engram of the workload's shape with
     row-sharded tables: forward with gradients (hash, differentiable row lookup, gate), backward
     from a fixed output gradient (gate backward, weight GEMMs, dedup of the row gradients), the
-    tables' gradient norm (clip, a host read) and the lazy row-wise Adam step with stochastic
-    rounding. The dense weights' gradients are dropped each step (their optimizer is not on the
-    lookup path)."""
+    tables' clip (norm, in-place scaling, a host read of the norm), the lazy row-wise Adam step
+    of the tables and the AdamW step of the dense key / value weights and scales, all with
+    stochastic rounding (the reference trainer's two optimizers, train/loop.py:299-302)."""
     eng = synthetic.build_engram("gemma", dev, seed=1)
     eng.shard_rows(0, 1, device=dev)
     rt = rows.RowTables([("model.layers.0.micro_engram.", eng)], lr=5e-3, lazy=True, rowwise=True,
                         sparse_grads=True, seed=2024)
+    dense = [eng.key.weight, eng.value.weight, eng.q_scale, eng.k_scale]
+    dense_opt = LazyAdamW(dense, lr=5e-3, lazy=False, seed=2025)
     gen = torch.Generator(device=dev).manual_seed(7)
     gout = torch.randn(batches[0][2].shape, generator=gen, device=dev).to(torch.bfloat16) * 1e-3
 
@@ -126,8 +136,8 @@ def training_step_ms(dev, batches, steps, warmup):
         eng(h, ids, pos).backward(gout)
         rt.clip(1.0)
         rt.step(5e-3)
-        for p in (eng.key.weight, eng.value.weight, eng.q_scale, eng.k_scale):
-            p.grad = None
+        dense_opt.step()
+        dense_opt.zero_grad(set_to_none=True)
 
     for k in range(warmup):
         step(k)
@@ -142,8 +152,23 @@ def training_step_ms(dev, batches, steps, warmup):
     return ms
 
 
-def cpu_baseline(eng, ids, pos, hidden, target_s):
-    """The oracle's CPU forward (C hash + torch-CPU embedding + inject) on a token sample."""
+def cpu_model():
+    """The host CPU's model name (first 'model name' of /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5):
+    """The reference path restated op for op in torch on the CPU (the oracle): hash_ids as
+    torch tensor ops (module.py:183-205) on the whole batch, then F.embedding lookups + inject
+    (module.py:146-154, 228-261) on a token sample; each timed as the median of `runs` runs
+    after one warm-up, with torch's intra-op threads = the host cores this process may use."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle
 
@@ -152,37 +177,47 @@ def cpu_baseline(eng, ids, pos, hidden, target_s):
     tables = [t.weight.detach().cpu() for t in eng.tables]
     wk, wv = eng.key.weight.detach().cpu(), eng.value.weight.detach().cpu()
     dq, dk = eng.q_scale.detach().cpu(), eng.k_scale.detach().cpu()
-    ids_np, pos_np = ids.cpu().numpy(), pos.cpu().numpy()
-    mults, canon = eng.mults.cpu().numpy(), eng.canon.cpu().numpy()
+    ids_c, pos_c = ids.cpu(), pos.cpu()
+    mults, canon = eng.mults.cpu(), eng.canon.cpu()
     h_all = hidden.reshape(-1, hidden.shape[-1]).cpu()
     T = h_all.shape[0]
 
-    t0 = time.perf_counter()
-    idx = oracle.hash_ids(ids_np, mults, eng._table_orders, eng.table_rows, canon, eng.pad_id,
-                          position_ids=pos_np).reshape(len(tables), -1)
-    hash_s_per_tok = (time.perf_counter() - t0) / T
+    def median_s(fn):
+        fn()  # warm-up
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times))
+
+    hash_out = {}
+
+    def hash_all():
+        hash_out["idx"] = oracle.hash_ids_torch(ids_c, mults, eng._table_orders, eng.table_rows,
+                                                canon, eng.pad_id, position_ids=pos_c)
+
+    hash_s_per_tok = median_s(hash_all) / T
+    idx = hash_out["idx"].reshape(len(tables), -1)
 
     def run(sample):
         mem = oracle.lookup_torch(tables, [i[sample] for i in idx])
         return oracle.inject(h_all[sample], mem, wk, wv, "scalar_sqrt", dq, dk)
 
     rng = np.random.Generator(np.random.PCG64(0))
-    probe = np.sort(rng.choice(T, 128, replace=False))
-    run(probe)  # warm-up
+    probe = torch.from_numpy(np.sort(rng.choice(T, 128, replace=False)))
+    run(probe)
     t0 = time.perf_counter()
     run(probe)
-    per_tok = (time.perf_counter() - t0) / probe.size
-    n = int(min(T, max(128, target_s / max(per_tok, 1e-9) / 3)))
-    sample = np.sort(rng.choice(T, n, replace=False))
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run(sample)
-        times.append(time.perf_counter() - t0)
-    per_tok = float(np.median(times)) / n + hash_s_per_tok
+    per_tok = (time.perf_counter() - t0) / probe.numel()
+    n = int(min(T, max(128, target_s / max(per_tok, 1e-9) / (runs + 1))))
+    sample = torch.from_numpy(np.sort(rng.choice(T, n, replace=False)))
+    per_tok = median_s(lambda: run(sample)) / n + hash_s_per_tok
     return {"value": 1.0 / per_tok, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} of the {T} tokens (3 runs, median) for lookup + inject; hash of all {T} "
-                      f"tokens in the C oracle (1 thread), per-token times added"}
+            "cpu_model": cpu_model(),
+            "sample": f"hash_ids as torch-CPU ops on all {T} tokens, then lookup + inject on {n} of "
+                      f"them; each the median of {runs} runs after 1 warm-up; per-token times "
+                      f"added"}
 
 
 def replay_ms(fns, reps):
@@ -209,6 +244,111 @@ def replay_ms(fns, reps):
         end.record(side)
         torch.cuda.synchronize()
     return start.elapsed_time(end) / (reps * len(fns))
+
+
+def graph_step_ms(step, n_steps):
+    """Wall-clock ms per call of step(k), k = 0 .. n_steps-1 captured as one HIP graph and
+    replayed once (synchronised on both sides), after an eager warm-up of each call."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for k in range(n_steps):
+            step(k)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for k in range(n_steps):
+                step(k)
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graph.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    del graph
+    return wall / n_steps * 1e3
+
+
+def measure_tiny(dev, steps=32, cycle=4):
+    """The tiny fp32 forward: one engram, orders {2,3}, 16 tables of 65,536 x 64 fp32, hidden
+    1024 fp32, one document of 2048 uniform ids over 32,000; `cycle` distinct seeded batches.
+    Forward tokens/s, the gather's HBM roofline and the projection's fp32 MFMA roofline."""
+    eng = synthetic.build_engram("tiny", dev, seed=0).eval()
+    batches = [tuple(t.to(dev) for t in synthetic.tiny_inputs(seed=s)) for s in range(cycle)]
+    T = batches[0][0].numel()
+    mems = [None] * cycle
+
+    def gather(k):
+        ids, pos, _ = batches[k % cycle]
+        mems[k % cycle] = eng.hashed_memory(ids, pos, dev)
+
+    def gate(k):
+        eng.gate_residual(batches[k % cycle][2], mems[k % cycle])
+
+    with torch.inference_mode():
+        ms = graph_step_ms(lambda k: (gather(k), gate(k)), steps)
+        gather_ms = replay_ms([(lambda k=k: gather(k)) for k in range(cycle)], 4)
+        gate_ms = replay_ms([(lambda k=k: gate(k)) for k in range(cycle)], 4)
+    M = len(eng.table_rows) * eng.engram_dim
+    d = batches[0][2].shape[-1]
+    gbytes = gather_bytes_per_token(eng, 4, False) * T
+    flop = 4.0 * M * d * T
+    out = {
+        "workload": "tiny_forward: 1 engram, orders {2,3}, 16 fp32 tables of 65536 x 64, hidden 1024 "
+                    "fp32, 1 x 2048 uniform ids over 32000, one document, scalar_sqrt gate",
+        "tokens_per_s": T / (ms * 1e-3), "ms_per_step": ms, "dtype": "f32",
+        "gather": {"mean_ms": gather_ms, "bytes_per_launch": gbytes,
+                   "achieved_gbs": gbytes / (gather_ms * 1e-3) / 1e9,
+                   "frac": gbytes / (gather_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "gate": {"mean_ms": gate_ms, "flop_per_launch": flop,
+                 "achieved_tflops": flop / (gate_ms * 1e-3) / 1e12, "peak_tflops": F32_PEAK_TFLOPS,
+                 "frac": flop / (gate_ms * 1e-3) / 1e12 / F32_PEAK_TFLOPS},
+    }
+    del eng, batches, mems
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_two_engram(dev, steps=3):
+    """Two Gemma-scale engrams (layers 0 and 29: seeds 0 and 290,203) with a canon map merging
+    15 % of the ids, prefill batch 8 x 8192 packed Zipf tokens, hidden 5376 bf16: the hidden
+    state through the first engram, then the second. Forward tokens/s of the chain and the
+    gather's HBM roofline (canon entry read per token)."""
+    rng = np.random.Generator(np.random.PCG64(29))
+    canon = synthetic.canon_map(rng, synthetic.GEMMA_VOCAB)
+    engs = [synthetic.build_engram("gemma", dev, seed=s, canon=canon).eval()
+            for s in (0, synthetic.LAYER29_SEED)]
+    ids, pos = synthetic.prefill_ids(seed=3, batch=8, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(4)
+    hidden = torch.randn(8, 8192, synthetic.GEMMA_DIM, generator=gen, device=dev).to(torch.bfloat16)
+    T = ids.numel()
+    state = {}
+
+    def chain(k):
+        h = hidden
+        for eng in engs:
+            h = eng(h, ids, pos)
+        state["out"] = h
+
+    def gather(k):
+        state["mem"] = engs[k % 2].hashed_memory(ids, pos, dev)
+
+    with torch.inference_mode():
+        ms = graph_step_ms(chain, steps)
+        gather_ms = replay_ms([(lambda k=k: gather(k)) for k in range(2)], 2)
+    gbytes = gather_bytes_per_token(engs[0], 2, not engs[0].identity_canon()) * T
+    out = {
+        "workload": "two_engram_canon: engrams of layers 0 and 29 (seeds 0, 290203), Gemma-scale "
+                    "tables each, canon map merging 15% of 262144 ids, batch 8 x 8192 packed Zipf(1.1), "
+                    "hidden 5376 bf16, chained",
+        "tokens_per_s": T / (ms * 1e-3), "ms_per_step": ms, "tokens_per_step": T, "dtype": "bf16",
+        "gather": {"mean_ms": gather_ms, "bytes_per_launch": gbytes,
+                   "achieved_gbs": gbytes / (gather_ms * 1e-3) / 1e9,
+                   "frac": gbytes / (gather_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+    }
+    del engs, hidden, state
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -314,6 +454,8 @@ def main():
         n_uniq = float(np.mean([u[4] for u in ubatches]))
         del ubatches, exp_avgs, exp_avg_sqs
     train_ms = training_step_ms(dev, batches, steps=10, warmup=3)
+    tiny = measure_tiny(dev)
+    two = measure_two_engram(dev)
     with torch.inference_mode():
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -404,6 +546,8 @@ def main():
             "step_us": decode_ms * 1e3,
             "tokens_per_s": decode_tokens / (decode_ms * 1e-3),
         },
+        "tiny_forward": tiny,
+        "two_engram_canon": two,
         "timing": "value: wall clock around one replay of a HIP graph of the K steps; kernel "
                   "durations: per-kernel graph replays over the 16 batches between HIP events",
         "cpu_baseline": None,

@@ -255,6 +255,18 @@ int me_sumsq(const float *x, int64_t n, float *out, int accumulate, void *worksp
              size_t workspace_size, void *stream);
 
 /*
+ * me_clip_scale -- the in-place scaling of RowTables.clip (micro_engram/rows.py:221-231):
+ * x *= coef with coef = min(max_norm * (1 / (sqrt(*sumsq) + 1e-6)), 1) in fp32 (torch evaluates
+ * the reference's max_norm / (norm + 1e-6) as a reciprocal and a product; a NaN norm gives a NaN
+ * coef). bf16 x is multiplied by coef rounded to bf16 (p.grad.mul_(coef.to(bf16))) and rounded.
+ *
+ *   x        [n] of dtype (ME_F32 / ME_BF16), 16-byte aligned, scaled in place
+ *   sumsq    device fp32 scalar: the squared gradient norm (me_sumsq)
+ *   max_norm > 0
+ */
+int me_clip_scale(void *x, int dtype, int64_t n, const float *sumsq, double max_norm, void *stream);
+
+/*
  * me_sparse_adam -- one LazyAdamW step on the given rows of n_tables tables.
  * Replaces the row branches of LazyAdamW.step (micro_engram/optim.py:65-133): with lazy != 0,
  * rows whose gradient is all zero are skipped (optim.py:88-104); weight decay, first moment, second moment (one
@@ -266,9 +278,6 @@ int me_sumsq(const float *x, int64_t n, float *out, int accumulate, void *worksp
  *   (device [rows_k] fp32 or [rows_k, dim] sq_dtype), rows (device int64 [n_rows_k], unique),
  *   grads (device fp32 [n_rows_k, dim]), n_rows, steps (the step count after this step's
  *   increment), stream_ids (< 65536, distinct per table: selects the table's rounding noise)
- *   grad_sumsq   nullable device fp32 scalar: gradients are scaled by
- *                min(max_norm / (sqrt(*grad_sumsq) + 1e-6), 1) first (RowTables.clip,
- *                rows.py:224-231)
  * The rounding noise of element (row, col) is 16 bits of Philox4x32-10 keyed by seed with counter
  * (row low, row high, step, stream_id << 16 | which << 14 | col >> 3), word (col >> 1) & 3,
  * half col & 1; which = 0 weights, 1 first moment, 2 per-value second moment.
@@ -278,8 +287,7 @@ int me_sparse_adam(int32_t n_tables, void *const *params, void *const *exp_avgs,
                    const int64_t *n_rows, const int64_t *steps, const int32_t *stream_ids,
                    int32_t dim, int param_dtype, int rowwise, int sq_dtype, int lazy, double lr,
                    double beta1, double beta2, double eps, double weight_decay,
-                   int stochastic_rounding, uint64_t seed, const float *grad_sumsq,
-                   double max_norm, void *stream);
+                   int stochastic_rounding, uint64_t seed, void *stream);
 
 /*
  * me_stochastic_bf16 -- fp32 -> bf16 with stochastic rounding (micro_engram/optim.py:33-44):

@@ -9,7 +9,8 @@ reference's MicroEngram module surface.
 The compute lives in libmicro_engram_amd.so (C-ABI: include/micro_engram.h), built in-tree by
 `python -m micro_engram_fork_amd._build`.
 """
-from .module import (MicroEngram, check_loaded, default_seed, engram_from_spec,  # noqa: F401
-                     resolve_order_sizes)
+from .module import (MicroEngram, attach_engram, check_loaded, default_seed,  # noqa: F401
+                     engram_from_spec, find_text_layers, layer_device_dtype, resolve_order_sizes)
 
-__all__ = ["MicroEngram", "check_loaded", "default_seed", "engram_from_spec", "resolve_order_sizes"]
+__all__ = ["MicroEngram", "attach_engram", "check_loaded", "default_seed", "engram_from_spec",
+           "find_text_layers", "layer_device_dtype", "resolve_order_sizes"]

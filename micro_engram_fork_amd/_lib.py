@@ -43,7 +43,8 @@ SIGNATURES = {
     "me_sumsq": [c_ptr, c_i64, c_ptr, c_int, c_ptr, c_size, c_ptr],
     "me_sparse_adam": [c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_int,
                        c_int, c_int, c_int, c_double, c_double, c_double, c_double, c_double,
-                       c_int, ctypes.c_uint64, c_ptr, c_double, c_ptr],
+                       c_int, ctypes.c_uint64, c_ptr],
+    "me_clip_scale": [c_ptr, c_int, c_i64, c_ptr, c_double, c_ptr],
     "me_stochastic_bf16": [c_ptr, c_i64, c_ptr, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                            c_ptr],
     "me_fill_engram_ids": [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_int, c_ptr, c_int, c_ptr, c_int,

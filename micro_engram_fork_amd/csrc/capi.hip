@@ -29,4 +29,4 @@ int check_launch(const char *what) {
 
 extern "C" const char *me_last_error(void) { return me::g_last_error.c_str(); }
 
-extern "C" int me_version(void) { return 1; }
+extern "C" int me_version(void) { return 2; }

@@ -7,6 +7,7 @@
 //              (zeros().index_add_(0, inv, g)): unique keys ascending, the inverse index, and the
 //              fp32 sum of each key's gradient rows in the order the rows appear
 //   sumsq      rows.py:214-220 (the squared norm RowTables.clip scales against)
+//   clip       rows.py:221-231 (the gradients scaled in place by min(max_norm / (norm + 1e-6), 1))
 //   adam       micro_engram/optim.py:65-133, the sparse-gradient branch (88-97), per-row second
 //              moment (112-114) and write-back with stochastic_bf16 (33-44, 120-132)
 //
@@ -768,6 +769,60 @@ __global__ __launch_bounds__(kSumBlocks) void sumsq_final(const float *partial, 
     if (tid == 0) *out = accumulate ? *out + s[0] : s[0];
 }
 
+// ---- clip: scale the gradients in place -------------------------------------------------------
+// RowTables.clip (rows.py:221-231): norm = sqrt(sumsq); coef = max_norm / (norm + 1e-6), which
+// torch evaluates as Tensor.__rtruediv__, i.e. reciprocal(norm + 1e-6) * max_norm, in fp32, then
+// clamp(max=1) (a NaN coef stays NaN); fp32 x *= coef, bf16 x *= coef rounded to bf16 first
+// (p.grad.mul_(coef.to(p.grad.dtype))), the product rounded to bf16. Every thread computes the
+// coefficient from the device scalar itself, so the host never reads the norm for this.
+__device__ __forceinline__ float clip_coef(const float *sumsq, float max_norm) {
+    const float r = 1.0f / (sqrtf(*sumsq) + 1e-6f);  // correctly rounded division and sqrt
+    const float c = r * max_norm;
+    return c > 1.0f ? 1.0f : c;
+}
+
+constexpr int kClipThreads = 256;
+
+// fp32: 4 values per 16-byte load; bf16: 8. Grid-stride over vectors, then a scalar tail.
+template <bool BF16>
+__global__ __launch_bounds__(kClipThreads) void clip_scale(void *x, int64_t n, const float *sumsq,
+                                                           float max_norm) {
+    float coef = clip_coef(sumsq, max_norm);
+    if (BF16) coef = round_to_bf16(coef);
+    constexpr int kPer = BF16 ? 8 : 4;
+    const int64_t nvec = n / kPer;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kClipThreads;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * kClipThreads + threadIdx.x;
+    gmem_ptr<u32x4_v> xv = as_global(reinterpret_cast<u32x4_v *>(x));
+    for (; i < nvec; i += stride) {
+        u32x4_v w = xv[i];
+        if (BF16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float lo = __uint_as_float(w[q] << 16) * coef;
+                const float hi = __uint_as_float(w[q] & 0xffff0000u) * coef;
+                w[q] = static_cast<uint32_t>(float_to_bf16_bits_rne(lo)) |
+                       (static_cast<uint32_t>(float_to_bf16_bits_rne(hi)) << 16);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) w[q] = __float_as_uint(__uint_as_float(w[q]) * coef);
+        }
+        xv[i] = w;
+    }
+    // the last n % kPer values: one thread each, in the first block
+    if (blockIdx.x == 0 && threadIdx.x < n - nvec * kPer) {
+        const int64_t j = nvec * kPer + threadIdx.x;
+        if (BF16) {
+            uint16_t *xb = static_cast<uint16_t *>(x);
+            xb[j] = float_to_bf16_bits_rne(bf16_bits_to_float(xb[j]) * coef);
+        } else {
+            float *xf = static_cast<float *>(x);
+            xf[j] = xf[j] * coef;
+        }
+    }
+}
+
 // ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ----------------------------------------
 __device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
     constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u;
@@ -835,8 +890,6 @@ struct AdamArgs {
     float decay;           // 1 - lr * weight_decay (1: no decay)
     int has_decay;
     float beta1, one_minus_beta1, beta2, one_minus_beta2, eps;
-    const float *sumsq;    // nullable: clip the gradients to max_norm against this squared norm
-    float max_norm;
 };
 
 __device__ __forceinline__ float load_elem(const uint8_t *base, int bf16, int64_t i) {
@@ -864,15 +917,11 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
     const int64_t row = *as_global(t.rows + i);
     const int D = a.dim;
     const float *g_row = t.grads + i * D;
-    float coef = 1.f;  // gradient clipping (rows.py:224-231): min(max_norm / (norm + 1e-6), 1)
-    if (a.sumsq != nullptr) coef = fminf(a.max_norm / (sqrtf(*a.sumsq) + 1e-6f), 1.0f);
-
     // lazy: a row whose gradient is all zero is skipped entirely (optim.py:92-95)
     bool any = false;
     float gsq = 0.f;
     for (int c = lane; c < D; c += 64) {
-        float g = g_row[c];
-        if (a.sumsq != nullptr) g *= coef;
+        const float g = g_row[c];
         any |= g != 0.f;
         gsq += g * g;
     }
@@ -890,8 +939,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
         denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
     }
     for (int c = lane; c < D; c += 64) {
-        float g = g_row[c];
-        if (a.sumsq != nullptr) g *= coef;
+        const float g = g_row[c];
         float p = load_elem(t.param, a.param_bf16, prow + c);
         float m = load_elem(t.exp_avg, a.param_bf16, prow + c);
         if (a.has_decay) p = p * a.decay;
@@ -1046,13 +1094,10 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
         load_cols<C, true>(t.exp_avg_sq, e0, v);
     else
         load_cols<C, false>(t.exp_avg_sq, e0, v);
-    float coef = 1.f;  // gradient clipping (rows.py:224-231): min(max_norm / (norm + 1e-6), 1)
-    if (a.sumsq != nullptr) coef = fminf(a.max_norm / (sqrtf(*a.sumsq) + 1e-6f), 1.0f);
     bool any = false;
     float gsq = 0.f;
 #pragma unroll
     for (int e = 0; e < C; ++e) {
-        if (a.sumsq != nullptr) g[e] *= coef;
         any |= g[e] != 0.f;
         gsq += g[e] * g[e];
     }
@@ -1325,6 +1370,28 @@ extern "C" int me_sumsq(const float *x, int64_t n, float *out, int accumulate, v
     return check_launch("me_sumsq");
 }
 
+extern "C" int me_clip_scale(void *x, int dtype, int64_t n, const float *sumsq, double max_norm,
+                             void *stream) {
+    ME_CHECK_ARG(n >= 0, "negative n");
+    ME_CHECK_ARG(x != nullptr || n == 0, "x is null");
+    ME_CHECK_ARG(sumsq != nullptr, "sumsq is null");
+    ME_CHECK_ARG(dtype == ME_F32 || dtype == ME_BF16, "x must be fp32 or bf16");
+    ME_CHECK_ARG(reinterpret_cast<uintptr_t>(x) % 16 == 0, "x must be 16-byte aligned");
+    ME_CHECK_ARG(max_norm > 0.0, "max_norm must be positive");
+    if (n == 0) return ME_OK;
+    const int per = dtype == ME_BF16 ? 8 : 4;
+    const int64_t blocks = std::min<int64_t>(std::max<int64_t>(ceil_div(n / per, kClipThreads), 1), 2048);
+    hipStream_t s = as_stream(stream);
+    const float mn = static_cast<float>(max_norm);
+    if (dtype == ME_BF16)
+        hipLaunchKernelGGL(clip_scale<true>, dim3(static_cast<unsigned>(blocks)), dim3(kClipThreads), 0,
+                           s, x, n, sumsq, mn);
+    else
+        hipLaunchKernelGGL(clip_scale<false>, dim3(static_cast<unsigned>(blocks)), dim3(kClipThreads), 0,
+                           s, x, n, sumsq, mn);
+    return check_launch("me_clip_scale");
+}
+
 template <int C, bool PB, bool RW>
 void launch_adam_vec_k(int lpr, dim3 grid, hipStream_t s, const AdamArgs &a) {
     switch (lpr) {
@@ -1352,8 +1419,7 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
                               const int64_t *steps, const int32_t *stream_ids, int32_t dim,
                               int param_dtype, int rowwise, int sq_dtype, int lazy, double lr,
                               double beta1, double beta2, double eps, double weight_decay,
-                              int stochastic_rounding, uint64_t seed, const float *grad_sumsq,
-                              double max_norm, void *stream) {
+                              int stochastic_rounding, uint64_t seed, void *stream) {
     ME_CHECK_ARG(n_tables >= 1 && n_tables <= 65536, "n_tables must be in [1, 65536]");
     ME_CHECK_ARG(params && exp_avgs && exp_avg_sqs && rows && grads && n_rows && steps && stream_ids,
                  "null argument array");
@@ -1375,8 +1441,6 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
     a.beta2 = static_cast<float>(beta2);
     a.one_minus_beta2 = static_cast<float>(1.0 - beta2);
     a.eps = static_cast<float>(eps);
-    a.sumsq = grad_sumsq;
-    a.max_norm = static_cast<float>(max_norm);
     for (int k = 0; k < n_tables; ++k) {
         ME_CHECK_ARG(n_rows[k] >= 0, "table %d: negative row count", k);
         ME_CHECK_ARG(steps[k] >= 1, "table %d: step must be >= 1", k);

@@ -213,6 +213,7 @@ class MicroEngram(nn.Module):
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):
+        self._canon_state = None  # a loaded canon map is checked again at the next hash
         for name in self.DELTA_SCALES:
             key = prefix + name
             if key in state_dict:
@@ -293,9 +294,19 @@ class MicroEngram(nn.Module):
                 return first.reshape(-1).as_strided((len(idx), n), (step // 8, 1))
         return torch.stack([i.reshape(-1).long() for i in idx])
 
+    def _served_memory(self, idx):
+        """The memory vectors [N, n_tables * D] through the installed row_lookup_fn: straight
+        from its concatenated buffer when it offers one (this package's tp_lookup), else the
+        concatenation of its per-table rows (module.py:149-150, 233)."""
+        fn = self.row_lookup_fn
+        memory = getattr(fn, "memory", None)
+        if memory is not None:
+            return memory(self, idx)
+        return torch.cat(fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
+
     def _mem(self, idx):
         if self.row_lookup_fn is not None and self.row_shards is not None:
-            return torch.cat(self.row_lookup_fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
+            return self._served_memory(idx)
         return ops.gather(self._stacked_idx(idx), self._table_weights())
 
     def _mem_grad(self, idx):
@@ -303,7 +314,7 @@ class MicroEngram(nn.Module):
         lookup of rows.py (dense table gradients, or sparse ones for row shards so marked)."""
         if self.row_shards is not None:
             if self.row_lookup_fn is not None:
-                return torch.cat(self.row_lookup_fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
+                return self._served_memory(idx)
             rank, world = self.row_info[0], self.row_info[1]
             if world != 1:
                 raise NotImplementedError(
@@ -468,3 +479,82 @@ SEED_STRIDE = 10007  # default seed of the engram at layer L is SEED_STRIDE * L 
 
 def default_seed(layer):
     return SEED_STRIDE * int(layer)
+
+
+# ------------------------------------------------------------------- attaching to a model
+def find_text_layers(model):
+    """(name, ModuleList) of the text decoder's layers (module.py:286-296): among the
+    ModuleLists whose name ends in "layers", the language model's if there is one, else the
+    first that belongs to neither a vision nor an audio tower."""
+    lists = [(name, mod) for name, mod in model.named_modules()
+             if isinstance(mod, nn.ModuleList) and name.endswith("layers")]
+    for name, mod in lists:
+        if "language_model" in name:
+            return name, mod
+    for name, mod in lists:
+        if "vision" not in name and "audio" not in name:
+            return name, mod
+    raise RuntimeError("[micro_engram] no text decoder layers found in the model; print(model) and "
+                       "pass the layer list yourself")
+
+
+# parameter classes of bitsandbytes whose dtype is a packed storage type, not the compute type
+_PACKED_PARAMS = ("Params4bit", "Int8Params")
+
+
+def layer_device_dtype(layer):
+    """(device, compute dtype) an engram placed in `layer` should take (module.py:334-352): the
+    first floating-point parameter that is not a packed quantized weight, else a submodule's
+    `compute_dtype`, else bf16 on the first parameter's device."""
+    params = list(layer.parameters())
+    if not params:
+        raise RuntimeError("[micro_engram] the decoder layer has no parameters")
+    for p in params:
+        if p.is_floating_point() and type(p).__name__ not in _PACKED_PARAMS:
+            return p.device, p.dtype
+    for mod in layer.modules():
+        dtype = getattr(mod, "compute_dtype", None)
+        if isinstance(dtype, torch.dtype) and dtype.is_floating_point:
+            return params[0].device, dtype
+    return params[0].device, torch.bfloat16
+
+
+def attach_engram(model, engram, layer_idx, dtype=None, get_ids=None):
+    """Place `engram` inside decoder layer `layer_idx` as its submodule `micro_engram` and add its
+    memory to the layer's output with a forward hook (module.py:355-393), so sharding,
+    offloading and checkpointing of that layer carry the engram with it.
+
+    The engram moves to the layer's device, in `dtype` or the layer's compute dtype (integer
+    buffers keep theirs). get_ids: a callable returning (input_ids, position_ids) for the
+    current forward; without it a pre-hook on `model` takes them from its forward's arguments
+    (keyword `input_ids` / `position_ids`, or the first positional argument). Returns the
+    layer's name and the hook handles."""
+    name, layers = find_text_layers(model)
+    layer = layers[layer_idx]
+    device, layer_dtype = layer_device_dtype(layer)
+    engram.to(device=device, dtype=dtype or layer_dtype)
+    layer.add_module("micro_engram", engram)
+    seen = {}
+
+    def remember_ids(_module, args, kwargs):
+        ids = kwargs.get("input_ids")
+        if ids is None and args:
+            ids = args[0]
+        seen["input_ids"] = ids
+        seen["position_ids"] = kwargs.get("position_ids")
+
+    def add_memory(_module, _args, output):
+        if get_ids is not None:
+            ids, pos = get_ids()
+        else:
+            ids, pos = seen.get("input_ids"), seen.get("position_ids")
+        if ids is None:
+            return output
+        if isinstance(output, tuple):
+            return (engram(output[0], ids, pos), *output[1:])
+        return engram(output, ids, pos)
+
+    handles = [layer.register_forward_hook(add_memory)]
+    if get_ids is None:
+        handles.append(model.register_forward_pre_hook(remember_ids, with_kwargs=True))
+    return f"{name}.{layer_idx}", handles

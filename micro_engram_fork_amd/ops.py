@@ -470,14 +470,29 @@ def sumsq(x, out=None, accumulate=False):
     return out
 
 
+def clip_scale(x, sumsq, max_norm):
+    """x *= min(max_norm / (sqrt(sumsq) + 1e-6), 1) in place, the scaling of RowTables.clip
+    (micro_engram/rows.py:221-231); x fp32 or bf16 and contiguous, sumsq a device fp32 scalar.
+    bf16 values are scaled by the coefficient rounded to bf16, as p.grad.mul_(coef.to(bf16))."""
+    dev = require_gpu(x, sumsq)
+    if not x.is_contiguous():
+        raise ValueError("[micro_engram] clip_scale needs a contiguous tensor (it scales in place)")
+    if x.data_ptr() % 16:
+        raise ValueError("[micro_engram] clip_scale needs a 16-byte aligned tensor")
+    if sumsq.dtype != torch.float32:
+        raise ValueError("[micro_engram] clip_scale: sumsq must be fp32")
+    call("me_clip_scale", x.data_ptr(), dtype_code(x), x.numel(), sumsq.data_ptr(), float(max_norm),
+         stream_of(dev))
+    return x
+
+
 def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *, lr, betas, eps,
-                weight_decay, rowwise, lazy, stochastic_rounding, seed, grad_sumsq=None,
-                max_norm=0.0):
+                weight_decay, rowwise, lazy, stochastic_rounding, seed):
     """One LazyAdamW step on the given rows of each table (micro_engram/optim.py:65-133), all
     tables in one launch. params/exp_avgs [rows_k, D]; exp_avg_sqs [rows_k] fp32 (row-wise) or
     like params; rows int64 [n_k] unique; grads fp32 [n_k, D]; steps: step counts after the
     increment. Updates the tensors in place."""
-    dev = require_gpu(*params, *exp_avgs, *exp_avg_sqs, *rows, *grads, grad_sumsq)
+    dev = require_gpu(*params, *exp_avgs, *exp_avg_sqs, *rows, *grads)
     n = len(params)
     if not (len(exp_avgs) == len(exp_avg_sqs) == len(rows) == len(grads) == len(steps) == n):
         raise ValueError("[micro_engram] sparse_adam: per-table lists differ in length")
@@ -505,7 +520,7 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
          i32_array([int(s) for s in stream_ids]), dim, dtype_code(params[0]), int(bool(rowwise)),
          sq_code, int(bool(lazy)), float(lr), float(betas[0]), float(betas[1]), float(eps),
          float(weight_decay), int(bool(stochastic_rounding)), int(seed) & ((1 << 64) - 1),
-         _p(grad_sumsq), float(max_norm), stream_of(dev))
+         stream_of(dev))
 
 
 def stochastic_bf16(x, seed, step=0, stream_id=0):

@@ -36,7 +36,6 @@ class LazyAdamW(torch.optim.Optimizer):
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, lazy=lazy,
                                       rowwise=rowwise, stochastic_rounding=stochastic_rounding))
         self.seed = int(torch.randint(0, 2**62, (1,)).item()) if seed is None else int(seed)
-        self._clip = None  # (device squared norm, max_norm) applied by the next step
 
     @staticmethod
     def init_state(state, p, group):
@@ -48,11 +47,6 @@ class LazyAdamW(torch.optim.Optimizer):
             state["exp_avg_sq"] = torch.zeros(p.shape[0], dtype=torch.float32, device=p.device)
         else:
             state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-
-    def clip_next_step(self, sumsq, max_norm):
-        """Scale the next step's gradients by min(max_norm / (sqrt(sumsq) + 1e-6), 1) inside the
-        update kernel (RowTables.clip, micro_engram/rows.py:224-231); sumsq is a device scalar."""
-        self._clip = (sumsq, float(max_norm))
 
     @staticmethod
     def _as_rows(t, n):
@@ -67,7 +61,6 @@ class LazyAdamW(torch.optim.Optimizer):
             with torch.enable_grad():
                 loss = closure()
         index = {id(p): i for i, p in enumerate(p for g in self.param_groups for p in g["params"])}
-        clip, self._clip = self._clip, None
         for group in self.param_groups:
             batches = {}
             for p in group["params"]:
@@ -94,7 +87,8 @@ class LazyAdamW(torch.optim.Optimizer):
                 V = state["exp_avg_sq"] if rowwise else self._as_rows(state["exp_avg_sq"], n)
                 key = (P.dtype, P.shape[1], rowwise, lazy, V.dtype)
                 b = batches.setdefault(key, {"params": [], "exp_avgs": [], "exp_avg_sqs": [], "rows": [],
-                                             "grads": [], "steps": [], "stream_ids": []})
+                                             "grads": [], "steps": [], "stream_ids": [], "written": []})
+                b["written"] += [p, state["exp_avg"], state["exp_avg_sq"]]
                 b["params"].append(P)
                 b["exp_avgs"].append(M)
                 b["exp_avg_sqs"].append(V)
@@ -107,6 +101,10 @@ class LazyAdamW(torch.optim.Optimizer):
                                 b["steps"], b["stream_ids"], lr=group["lr"], betas=group["betas"],
                                 eps=group["eps"], weight_decay=group["weight_decay"], rowwise=rowwise,
                                 lazy=lazy, stochastic_rounding=group.get("stochastic_rounding", True),
-                                seed=self.seed, grad_sumsq=clip[0] if clip else None,
-                                max_norm=clip[1] if clip else 0.0)
+                                seed=self.seed)
+                # the kernel wrote through raw pointers: move the version counters as torch's
+                # own in-place ops would (autograd's saved-tensor checks and caches keyed on
+                # them -- the engram's stacked key/value weight -- then see the update)
+                # (p itself: p.data has a version counter of its own)
+                torch.autograd.graph.increment_version(b["written"])
         return loss

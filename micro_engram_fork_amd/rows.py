@@ -182,23 +182,31 @@ class RowTables:
         return [p for _, e in self.entries for p in e.row_shards]
 
     def clip(self, max_norm):
-        """Global norm of the table gradients; the next step scales them to max_norm if larger
-        (rows.py:208-233). Returns the norm (a host read, as in the reference)."""
+        """Global norm of the table gradients, and the gradients scaled down in place to
+        max_norm if it is larger (rows.py:208-233): dense p.grad and sparse_grad sums alike, by
+        min(max_norm / (norm + 1e-6), 1), computed on the device from the norm (no host read
+        before the scaling). Returns the norm (a host read, as in the reference)."""
         ps = [p for p in self.params() if p.requires_grad]
         if not ps:
             return None
         sq = torch.zeros(1, dtype=torch.float32, device=ps[0].device)
-        parts = []
+        squares, scaled = [], []
         for p in ps:
             if p.grad is not None:
-                parts.append(p.grad)
+                squares.append(p.grad if p.grad.dtype == torch.float32 else p.grad.float())
+                scaled.append(p.grad)
             sg = getattr(p, "sparse_grad", None)
             if sg is not None:
-                parts.append(sg[1])
-        for span in _spans(parts):
+                squares.append(sg[1])
+                scaled.append(sg[1])
+        for span in _spans(squares):
             ops.sumsq(span, sq, accumulate=True)
-        if max_norm and max_norm > 0 and self.optimizer is not None:
-            self.optimizer.clip_next_step(sq, max_norm)
+        if max_norm and max_norm > 0:
+            for span in _spans(scaled):
+                if span.is_contiguous() and span.data_ptr() % 16 == 0:
+                    ops.clip_scale(span, sq, max_norm)
+                else:  # a view the kernel cannot scale in place: scale a copy, write it back
+                    span.copy_(ops.clip_scale(span.contiguous().clone(), sq, max_norm))
         self.last_grad_norm = float(sq.sqrt().item())
         return self.last_grad_norm
 
@@ -216,105 +224,122 @@ class RowTables:
         for p in self.params():
             p.sparse_grad = None
 
-    # --- checkpoints (DCP folders the reference's loaders and RowTables.load read) ---
-    def _table_items(self, frozen_too=False):
-        """(full name of table k, rows, row shard) of every engram with trainable rows."""
-        for prefix, e in self.entries:
-            if not frozen_too and not any(p.requires_grad for p in e.row_shards):
-                continue
-            for k, p in enumerate(e.row_shards):
-                yield f"{prefix}tables.{k}.weight", e.table_rows[k], p
+    # --- checkpoints: DCP folders (rows.py:257-343 fixes their names and contents) ---------
+    def _trainable_tables(self, include_frozen=False):
+        """(name in the checkpoint, shard) of every table of the engrams that train rows."""
+        for prefix, engram in self.entries:
+            if include_frozen or any(p.requires_grad for p in engram.row_shards):
+                for k, shard in enumerate(engram.row_shards):
+                    yield f"{prefix}tables.{k}.weight", shard
 
     def save(self, folder, optim_folder=None):
-        """The complete engrams (tables + key/value/scales/buffers under their full names) to the
-        DCP folder `folder`, and the tables' optimizer state (exp_avg, exp_avg_sq, step per
-        table) to `optim_folder` (rows.py:258-281). Engrams whose rows are frozen are skipped.
-        On one GPU every shard is its whole table, so the tensors are written as they are."""
+        """Write the engrams that train rows, complete (their tables and every other tensor under
+        full names, the scales as 1 + delta), to the DCP folder `folder`; and the tables'
+        optimizer state -- <table name>.exp_avg, .exp_avg_sq and .step -- to `optim_folder`.
+        With one GPU each shard is a whole table and is written as it is."""
         import torch.distributed.checkpoint as dcp
 
-        sd = {}
-        for prefix, e in self.entries:
-            if any(p.requires_grad for p in e.row_shards):
-                sd.update({prefix + k: v.detach() for k, v in e.state_dict().items()})
-        for key, _rows, p in self._table_items():
-            sd[key] = p.detach()
-        if sd:
-            dcp.save(sd, checkpoint_id=folder, no_dist=True)
-        if optim_folder and self.optimizer is not None:
-            osd = {}
-            for key, _rows, p in self._table_items():
-                st = self.optimizer.state.get(p)
-                if st:
-                    osd[f"{key}.exp_avg"] = st["exp_avg"]
-                    osd[f"{key}.exp_avg_sq"] = st["exp_avg_sq"]
-                    osd[f"{key}.step"] = st["step"].detach().clone().reshape(())
-            if osd:
-                dcp.save(osd, checkpoint_id=optim_folder, no_dist=True)
+        tensors = {}
+        for prefix, engram in self.entries:
+            if any(p.requires_grad for p in engram.row_shards):
+                tensors.update((prefix + k, v.detach()) for k, v in engram.state_dict().items())
+        tensors.update((name, shard.detach()) for name, shard in self._trainable_tables())
+        if tensors:
+            dcp.save(tensors, checkpoint_id=folder, no_dist=True)
+        if not optim_folder or self.optimizer is None:
+            return
+        state = {}
+        for name, shard in self._trainable_tables():
+            st = self.optimizer.state.get(shard)
+            if st:
+                state[name + ".exp_avg"] = st["exp_avg"]
+                state[name + ".exp_avg_sq"] = st["exp_avg_sq"]
+                state[name + ".step"] = st["step"].detach().clone().reshape(())
+        if state:
+            dcp.save(state, checkpoint_id=optim_folder, no_dist=True)
+
+    def _locate_tables(self, folder, meta):
+        """{name in the folder: shard to fill} for every table of every engram. A table is found
+        under the engram's own layer, else under a name without a layer; its row count must be
+        the engram's (a run cannot resume onto tables of another size)."""
+        from .weights import EngramKey
+
+        saved = {}
+        for name in meta:
+            key = EngramKey.parse(name)
+            if key is not None and key.local.startswith("tables."):
+                saved[(key.layer, key.local)] = name
+        plan = {}
+        for prefix, engram in self.entries:
+            layer = EngramKey.parse(prefix + "x")
+            layer = None if layer is None else layer.layer
+            for k, shard in enumerate(engram.row_shards):
+                local = f"tables.{k}.weight"
+                name = saved.get((layer, local)) or saved.get((None, local))
+                if name is None:
+                    raise ValueError(f"[micro_engram] {folder} holds no {local} for the engram at "
+                                     f"{prefix.rstrip('.')}")
+                rows = meta[name].size[0]
+                if rows != engram.table_rows[k]:
+                    raise ValueError(
+                        f"[micro_engram] {folder}: {local} was saved with {rows:,} rows; this engram's "
+                        f"table {k} (order {engram._table_orders[k]}) has {engram.table_rows[k]:,}. "
+                        "Resuming needs the same table sizes.")
+                plan[name] = shard
+        return plan
 
     def load(self, folder, optim_folder=None):
-        """Tables from a DCP folder (a micro_engram_rows folder, or an FSDP checkpoint of a run
-        without row sharding), read into the row shards in place; optimizer state from
-        optim_folder when it exists, the second moment converted when it was saved by the other
-        optimizer (per value <-> per row). Returns (tables loaded, optimizer state loaded)
-        (rows.py:283-343)."""
+        """Fill the row shards in place from a DCP folder -- a micro_engram_rows folder, or the
+        model checkpoint of a run that did not shard rows -- and, when `optim_folder` exists, the
+        tables' optimizer state, converting the second moment if the other optimizer wrote it
+        (per value <-> per row). Returns (tables loaded, whether optimizer state was loaded)."""
         import torch.distributed.checkpoint as dcp
 
-        from .weights import layer_of_key, local_name
-
         meta = dcp.FileSystemReader(folder).read_metadata().state_dict_metadata
-        by_name = {}
-        for k in meta:
-            local = local_name(k)
-            if local is not None and local.startswith("tables."):
-                by_name[(layer_of_key(k), local)] = k
-        want = {}
-        for prefix, e in self.entries:
-            layer = layer_of_key(prefix + "x")
-            for k, p in enumerate(e.row_shards):
-                name = f"tables.{k}.weight"
-                found = by_name.get((layer, name)) or by_name.get((None, name))
-                if found is None:
-                    raise ValueError(f"[micro_engram] {folder} has no {name} for {prefix.rstrip('.')}")
-                saved_rows = meta[found].size[0]
-                if saved_rows != e.table_rows[k]:
-                    raise ValueError(f"[micro_engram] {folder}: {name} has {saved_rows:,} rows, this engram's "
-                                     f"table {k} (order {e._table_orders[k]}) has {e.table_rows[k]:,}: "
-                                     f"different table sizes can't resume (start a new run, or keep the sizes)")
-                want[found] = p
-        dcp.load({k: p.data for k, p in want.items()}, checkpoint_id=folder, no_dist=True)
+        plan = self._locate_tables(folder, meta)
+        dcp.load({name: shard.data for name, shard in plan.items()}, checkpoint_id=folder, no_dist=True)
         self.converted = 0
-        if not (optim_folder and self.optimizer is not None and os.path.isdir(optim_folder)):
-            return len(want), False
-        ometa = dcp.FileSystemReader(optim_folder).read_metadata().state_dict_metadata
-        templ, steps, convert = {}, {}, {}
+        if optim_folder and self.optimizer is not None and os.path.isdir(optim_folder):
+            return len(plan), self._load_optimizer(optim_folder)
+        return len(plan), False
+
+    def _load_optimizer(self, optim_folder):
+        import torch.distributed.checkpoint as dcp
+
+        meta = dcp.FileSystemReader(optim_folder).read_metadata().state_dict_metadata
         group = self.optimizer.param_groups[0]
-        for key, _rows, p in self._table_items():
-            if f"{key}.exp_avg" not in ometa:
+        targets, steps, foreign = {}, {}, {}
+        for name, shard in self._trainable_tables():
+            if name + ".exp_avg" not in meta:
                 continue
-            st = self.optimizer.state[p]
+            st = self.optimizer.state[shard]
             if not st:
-                LazyAdamW.init_state(st, p, group)
-            templ[f"{key}.exp_avg"] = st["exp_avg"]
-            saved_dims = len(ometa[f"{key}.exp_avg_sq"].size)
-            sq = st["exp_avg_sq"]
-            if saved_dims != sq.dim():  # written by the other optimizer (lazy <-> rowwise)
-                sq = torch.zeros(p.shape if saved_dims == p.dim() else p.shape[:1], dtype=torch.float32,
-                                 device=p.device)
-                convert[p] = sq
-            templ[f"{key}.exp_avg_sq"] = sq
-            templ[f"{key}.step"] = steps[p] = torch.zeros((), dtype=torch.float32)
-        if not templ:
-            return len(want), False
-        dcp.load(templ, checkpoint_id=optim_folder, no_dist=True)
-        for p, s in steps.items():
-            self.optimizer.state[p]["step"] = s
-        for p, sq in convert.items():
-            st = self.optimizer.state[p]
-            if sq.dim() > st["exp_avg_sq"].dim():
-                # per value -> per row: v is linear in g^2, so the row mean of the per-value
-                # moments is exactly the row-wise moment
-                st["exp_avg_sq"].copy_(sq.flatten(1).mean(dim=1))
-            else:  # per row -> per value: every value of the row takes the row's moment
-                st["exp_avg_sq"].copy_(sq.reshape(-1, *([1] * (p.dim() - 1))).expand_as(p))
-        self.converted = len(convert)
-        return len(want), True
+                LazyAdamW.init_state(st, shard, group)
+            targets[name + ".exp_avg"] = st["exp_avg"]
+            saved_dims = len(meta[name + ".exp_avg_sq"].size)
+            if saved_dims == st["exp_avg_sq"].dim():
+                targets[name + ".exp_avg_sq"] = st["exp_avg_sq"]
+            else:  # the other optimizer's layout: read it as saved, convert below
+                shape = shard.shape if saved_dims == shard.dim() else shard.shape[:1]
+                foreign[shard] = torch.zeros(shape, dtype=torch.float32, device=shard.device)
+                targets[name + ".exp_avg_sq"] = foreign[shard]
+            steps[shard] = targets[name + ".step"] = torch.zeros((), dtype=torch.float32)
+        if not targets:
+            return False
+        dcp.load(targets, checkpoint_id=optim_folder, no_dist=True)
+        for shard, step in steps.items():
+            self.optimizer.state[shard]["step"] = step
+        for shard, saved in foreign.items():
+            self.optimizer.state[shard]["exp_avg_sq"].copy_(_convert_second_moment(saved, shard))
+        self.converted = len(foreign)
+        return True
+
+
+def _convert_second_moment(saved, shard):
+    """The second moment one optimizer saved, in the layout of the other (rows.py:330-339).
+    Per value -> per row: the row mean, which is exactly what the row-wise optimizer keeps (the
+    moment is linear in g^2 and the row-wise one averages g^2 over the row). Per row -> per
+    value: every value of a row takes the row's moment."""
+    if saved.dim() == shard.dim():
+        return saved.flatten(1).mean(dim=1)
+    return saved.reshape(-1, *([1] * (shard.dim() - 1))).expand_as(shard)

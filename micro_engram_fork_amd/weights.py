@@ -1,415 +1,435 @@
-"""Engram weights on disk: the files micro-engram writes, read back into a MicroEngram.
+"""Engram weights on disk: reading the files a trained engram is kept in, and writing them.
 
-Tensors are named relative to the engram (tables.0.weight, key.weight, value.weight,
-q_scale, k_scale, mults, canon), or with the full name of the model they sit in
-(model.language_model.layers.29.micro_engram.tables.0.weight; FSDP inserts
-_checkpoint_wrapped_module before micro_engram). The scales are stored as the scale itself
-(1 + delta, fp32); MicroEngram's state-dict hooks convert (micro_engram/module.py:156-181).
+What is on disk is fixed by the reference (micro_engram/weights.py:112-202, runconfig.py:40-67,
+module.py:166-181); how it is read here is this package's own:
 
-Formats read (micro_engram/weights.py:112-142):
-  *.pt                      torch.save of a dict (micro_engram.pt: local names; nested dicts
-                            are flattened with dots). Read with weights_only=True: nothing in
-                            the file is executed.
-  *.safetensors             one file, full or local names
-  folder of *.safetensors   a merged or assembled model (only engram tensors are read)
-  DCP folder (.metadata)    torch.distributed.checkpoint, e.g. checkpoint-N/pytorch_model_fsdp_0
-                            or micro_engram_rows; only the engram tensors are read, in one
-                            process (no process group)
-Formats written (save_engram_weights): the same four, so a trained engram leaves this package
-in a form the reference's loaders read.
+  * an engram tensor is named either locally ("tables.0.weight", "key.weight", "q_scale",
+    "mults", "canon", ...) or by its place in a model, "<...>.layers.<L>.micro_engram.<local>",
+    possibly with FSDP's "_checkpoint_wrapped_module." before "micro_engram" -- EngramKey
+    parses both;
+  * the scales are stored as the scale itself (1 + the module's delta, fp32); MicroEngram's
+    state-dict hooks convert;
+  * four containers hold the tensors -- a torch.save'd dict (.pt, read with weights_only=True,
+    so nothing in the file runs; nested dicts flatten with dots), one .safetensors file, a
+    folder of .safetensors files (a merged or assembled model), and a torch.distributed
+    checkpoint folder (a ".metadata" file: a trainer's pytorch_model_fsdp_0 or a
+    micro_engram_rows folder), read in this process without a process group. Each is a
+    TensorSource: list the names, read the ones wanted.
 
-micro_engram_config.json (micro_engram/weights.py:152-246, runconfig.py:40-67) says which
-engrams a run has (layer, sizes, orders, gate, seed, canon, weights path); engram_specs and
-resolve_engram_source turn it into constructor arguments for engram_from_spec.
+micro_engram_config.json describes a run's engrams (layer, sizes, orders, gate, seed, canon,
+weights); engram_specs turns it into one settings dict per engram for engram_from_spec, and
+resolve_engram_source finds the config and weights of a layer from a config file, a checkpoint
+folder, a training output folder or the weights themselves.
 """
 import glob
-import hashlib
 import json
 import os
 import re
 
 import torch
 
-from .module import SEED_STRIDE, default_seed  # noqa: F401  (re-exported: weights.py:152-160)
+from .module import SEED_STRIDE, default_seed  # noqa: F401  (the seed rule, weights.py:157)
 
-TAG = "micro_engram."
 CONFIG_NAME = "micro_engram_config.json"
-ENGRAM_FILE = "micro_engram.safetensors"  # assemble_engram_model.py:37
+ENGRAM_FILE = "micro_engram.safetensors"  # an assembled model's engram file
+MODULE_NAME = "micro_engram"
 
-# decoder layer of a full name: "...layers.<L>.[_checkpoint_wrapped_module.]micro_engram."
-_LAYER_KEY = re.compile(r"(?:^|\.)layers\.(\d+)\.(?:_checkpoint_wrapped_module\.)?micro_engram\.")
-_CHECKPOINT_DIR = re.compile(r"checkpoint-(\d+)$")
-_SPEC_FIELDS = ("layer", "table_size", "table_sizes", "engram_dim", "num_heads", "orders", "gate",
-                "seed", "pad_id", "token_merge", "canon_path", "frozen", "init_from")
+# ".layers.<L>." then an optional FSDP wrapper, then the engram module
+_PLACED = re.compile(r"(?:^|\.)layers\.(?P<layer>\d+)\.(?:_checkpoint_wrapped_module\.)?"
+                     + MODULE_NAME + r"\.(?P<local>.+)$")
+_CHECKPOINT = re.compile(r"^checkpoint-(\d+)$")
 
-
-# ----------------------------------------------------------------------------- tensor names
-def local_name(key):
-    """Name inside the engram ('tables.0.weight') of a full tensor name, or None when the key is
-    not an engram tensor (weights.py:28-36)."""
-    mark = "." + TAG
-    if mark in key:
-        return key.split(mark, 1)[1]
-    return key[len(TAG):] if key.startswith(TAG) else None
+# settings an engram entry of the config may carry (the rest of a config is not the engram's)
+SPEC_KEYS = ("layer", "table_size", "table_sizes", "engram_dim", "num_heads", "orders", "gate",
+             "seed", "pad_id", "token_merge", "canon_path", "frozen", "init_from")
 
 
-def layer_of_key(key):
-    """Decoder layer a full engram tensor name belongs to, or None (weights.py:39-45)."""
-    m = _LAYER_KEY.search(key)
-    return None if m is None else int(m.group(1))
+# ------------------------------------------------------------------------------ names
+class EngramKey:
+    """A parsed tensor name: `local` is the name inside the engram, `layer` the decoder layer
+    (None for local names and for names under a bare "micro_engram." prefix)."""
+
+    __slots__ = ("layer", "local")
+
+    def __init__(self, layer, local):
+        self.layer, self.local = layer, local
+
+    @classmethod
+    def parse(cls, name):
+        """The EngramKey of `name`, or None for tensors that are not an engram's."""
+        m = _PLACED.search(name)
+        if m is not None:
+            return cls(int(m.group("layer")), m.group("local"))
+        head = MODULE_NAME + "."
+        if name.startswith(head):
+            return cls(None, name[len(head):])
+        mid = "." + head
+        if mid in name:
+            return cls(None, name.split(mid, 1)[1])
+        return None
+
+    def belongs_to(self, layer):
+        """Whether the tensor is part of decoder `layer`'s engram: any engram when layer is None;
+        a name without a layer fits every layer."""
+        return layer is None or self.layer is None or self.layer == layer
 
 
-def _is_wanted(key, layer):
-    """An engram tensor of `layer` (of any layer when None; names without a layer always)."""
-    if local_name(key) is None:
-        return False
-    found = layer_of_key(key)
-    return layer is None or found is None or found == layer
+def local_name(name):
+    """Name of an engram tensor inside the engram, or None when `name` is not one."""
+    key = EngramKey.parse(name)
+    return None if key is None else key.local
+
+
+def layer_of_key(name):
+    """Decoder layer of a full engram tensor name, or None."""
+    key = EngramKey.parse(name)
+    return None if key is None else key.layer
 
 
 def full_name(layer, local, prefix="model.language_model.layers"):
-    """The name an engram tensor has inside a model: <prefix>.<layer>.micro_engram.<local>."""
-    return f"{prefix}.{int(layer)}.{TAG}{local}"
+    """The name the tensor `local` of decoder `layer`'s engram has inside a model."""
+    return f"{prefix}.{int(layer)}.{MODULE_NAME}.{local}"
 
 
-def _flatten(tree, prefix=""):
-    flat = {}
-    for k, v in tree.items():
-        if isinstance(v, dict):
-            flat.update(_flatten(v, f"{prefix}{k}."))
-        else:
-            flat[f"{prefix}{k}"] = v
-    return flat
+# ------------------------------------------------------------------------------ containers
+class TensorSource:
+    """A weights container: names() lists every tensor name in it, read(names) returns
+    {name: CPU tensor} for the ones asked for."""
+
+    def __init__(self, path):
+        self.path = path
+
+    def names(self):
+        raise NotImplementedError
+
+    def read(self, names):
+        raise NotImplementedError
 
 
-def _localised(sd, layer):
-    return {local_name(k): v for k, v in sd.items() if torch.is_tensor(v) and _is_wanted(k, layer)}
+class _DcpSource(TensorSource):
+    def _meta(self):
+        import torch.distributed.checkpoint as dcp
+
+        return dcp.FileSystemReader(self.path).read_metadata().state_dict_metadata
+
+    def names(self):
+        from torch.distributed.checkpoint.metadata import TensorStorageMetadata
+
+        return [k for k, m in self._meta().items() if isinstance(m, TensorStorageMetadata)]
+
+    def read(self, names):
+        import torch.distributed.checkpoint as dcp
+
+        meta = self._meta()
+        out = {k: torch.empty(tuple(meta[k].size), dtype=meta[k].properties.dtype) for k in names}
+        if out:
+            dcp.load(out, storage_reader=dcp.FileSystemReader(self.path), no_dist=True)
+        return out
 
 
-# ----------------------------------------------------------------------------- readers
-def _is_dcp(path):
+class _SafetensorsSource(TensorSource):
+    def __init__(self, path, files):
+        super().__init__(path)
+        self.files = files
+
+    def _index(self):
+        from safetensors import safe_open
+
+        where = {}
+        for f in self.files:
+            with safe_open(f, framework="pt", device="cpu") as fh:
+                for k in fh.keys():
+                    where[k] = f
+        return where
+
+    def names(self):
+        return list(self._index())
+
+    def read(self, names):
+        from safetensors import safe_open
+
+        by_file = {}
+        index = self._index()
+        for k in names:
+            by_file.setdefault(index[k], []).append(k)
+        out = {}
+        for f, ks in by_file.items():
+            with safe_open(f, framework="pt", device="cpu") as fh:
+                out.update({k: fh.get_tensor(k) for k in ks})
+        return out
+
+
+class _PtSource(TensorSource):
+    def _flat(self):
+        if getattr(self, "_loaded", None) is not None:
+            return self._loaded
+        tree = torch.load(self.path, map_location="cpu", weights_only=True)
+        flat, todo = {}, [("", tree)]
+        while todo:
+            prefix, node = todo.pop()
+            for k, v in node.items():
+                if isinstance(v, dict):
+                    todo.append((f"{prefix}{k}.", v))
+                elif torch.is_tensor(v):
+                    flat[f"{prefix}{k}"] = v
+        self._loaded = flat
+        return flat
+
+    def names(self):
+        return list(self._flat())
+
+    def read(self, names):
+        flat = self._flat()
+        return {k: flat[k] for k in names}
+
+
+def open_source(path):
+    """The TensorSource for `path`: a DCP folder (it has .metadata), a folder of .safetensors, a
+    .safetensors file, or anything else as a torch.save'd dict."""
+    path = os.path.abspath(path)
+    if os.path.isdir(path):
+        if os.path.isfile(os.path.join(path, ".metadata")):
+            return _DcpSource(path)
+        return _SafetensorsSource(path, sorted(glob.glob(os.path.join(path, "*.safetensors"))))
+    if path.endswith(".safetensors"):
+        return _SafetensorsSource(path, [path])
+    return _PtSource(path)
+
+
+def is_dcp_folder(path):
     return os.path.isdir(path) and os.path.isfile(os.path.join(path, ".metadata"))
 
 
-def _safetensors_files(path):
-    return sorted(glob.glob(os.path.join(path, "*.safetensors"))) if os.path.isdir(path) else [path]
-
-
-def _read_dcp(folder, layer):
-    """Only the engram tensors of a DCP checkpoint, read in this process (weights.py:59-73)."""
-    import torch.distributed.checkpoint as dcp
-    from torch.distributed.checkpoint.metadata import TensorStorageMetadata
-
-    reader = dcp.FileSystemReader(folder)
-    meta = reader.read_metadata().state_dict_metadata
-    out = {k: torch.empty(tuple(m.size), dtype=m.properties.dtype) for k, m in meta.items()
-           if isinstance(m, TensorStorageMetadata) and _is_wanted(k, layer)}
-    if out:
-        dcp.load(out, storage_reader=reader, no_dist=True)
-    return _localised(out, layer)
-
-
-def _read_safetensors(files, layer):
-    from safetensors import safe_open
-
-    out = {}
-    for f in files:
-        with safe_open(f, framework="pt", device="cpu") as fh:
-            for k in fh.keys():
-                if _is_wanted(k, layer):
-                    out[local_name(k)] = fh.get_tensor(k)
-    return out
-
-
-def _unlayered(sd, path, layer, need_layer):
-    """A file saved with local names carries no layer; shared by several engrams it would give
-    each the same tensors, so that is an error when need_layer (weights.py:144-150)."""
-    if need_layer and layer is not None and any(k.startswith("tables.") for k in sd):
-        raise ValueError(f"[micro_engram] {path} is used by several engrams, but its tensor names have "
-                         f"no layer number (e.g. {next(iter(sd))}), so it can't tell which is layer "
-                         f"{layer}'s. Give each engram its own file, or keep the full names "
-                         f"(...layers.{layer}.micro_engram.tables.0.weight)")
-    return sd
-
-
+# ------------------------------------------------------------------------------ reading
 def load_engram_weights(path, layer=None, need_layer=False):
-    """{local name: CPU tensor} of the engram stored at `path` (a .pt, a .safetensors file, a
-    folder of .safetensors, or a DCP folder); with `layer`, only that decoder layer's engram
-    (weights.py:112-141)."""
-    path = os.path.abspath(path)
-    if _is_dcp(path):
-        return _read_dcp(path, layer)
-    if os.path.isdir(path):
-        return _read_safetensors(_safetensors_files(path), layer)
-    if path.endswith(".safetensors"):
-        sd = _read_safetensors([path], layer)
-        if sd:
-            return sd
-        from safetensors.torch import load_file
-
-        return _unlayered(load_file(path), path, layer, need_layer)
-    tree = torch.load(path, map_location="cpu", weights_only=True)
-    flat = _flatten(tree)
-    sd = _localised(flat, layer)
-    if sd:
-        return sd
-    return _unlayered({k: v for k, v in flat.items() if torch.is_tensor(v)}, path, layer, need_layer)
+    """{local name: CPU tensor} of the engram stored at `path`, only decoder `layer`'s engram when
+    a layer is given. A file of plain local names (no "micro_engram." anywhere, like
+    micro_engram.pt) is the engram itself; if it may be shared by several engrams
+    (need_layer with a layer given), it cannot tell which layer it is for and is refused."""
+    src = open_source(path)
+    names = src.names()
+    wanted = {}
+    for name in names:
+        key = EngramKey.parse(name)
+        if key is not None and key.belongs_to(layer):
+            wanted[name] = key.local
+    if wanted:
+        return {wanted[k]: v for k, v in src.read(list(wanted)).items()}
+    if os.path.isdir(src.path):
+        return {}  # a checkpoint or model folder without this engram
+    # a single file with nothing named as an engram tensor holds the engram under local names
+    if need_layer and layer is not None and any(n.startswith("tables.") for n in names):
+        raise ValueError(
+            f"[micro_engram] {path} names its tensors without a decoder layer ({names[0]}, ...), and "
+            f"several engrams read it: there is no telling which tensors are layer {layer}'s. Save "
+            f"each engram to its own file, or under full names (...layers.{layer}.micro_engram.*)")
+    return src.read(names)
 
 
 def engram_layers_in(path):
-    """Sorted decoder layers whose engram tensors are stored at `path` (weights.py:88-109)."""
-    path = os.path.abspath(path)
-    if _is_dcp(path):
-        import torch.distributed.checkpoint as dcp
-
-        keys = list(dcp.FileSystemReader(path).read_metadata().state_dict_metadata)
-    elif os.path.isdir(path) or path.endswith(".safetensors"):
-        from safetensors import safe_open
-
-        keys = []
-        for f in _safetensors_files(path):
-            with safe_open(f, framework="pt", device="cpu") as fh:
-                keys.extend(fh.keys())
-    else:
-        keys = list(_flatten(torch.load(path, map_location="cpu", weights_only=True)))
-    return sorted({layer_of_key(k) for k in keys
-                   if local_name(k) is not None and layer_of_key(k) is not None})
+    """The decoder layers, sorted, that have engram tensors at `path`."""
+    layers = set()
+    for name in open_source(path).names():
+        key = EngramKey.parse(name)
+        if key is not None and key.layer is not None:
+            layers.add(key.layer)
+    return sorted(layers)
 
 
-# ----------------------------------------------------------------------------- writers
+# ------------------------------------------------------------------------------ writing
 def engram_state(engram):
-    """The engram's tensors under their local names, on the CPU, scales as 1 + delta (fp32). A
-    row-sharded engram on one GPU contributes its row shards as the tables."""
-    sd = {k: v.detach().cpu() for k, v in engram.state_dict().items()}
-    shards = getattr(engram, "row_shards", None)
-    if shards is not None:
-        for k, p in enumerate(shards):
-            sd[f"tables.{k}.weight"] = p.detach().cpu()
-    return sd
+    """The engram's tensors under local names on the CPU, scales as 1 + delta in fp32; a
+    row-sharded engram on one GPU gives its shards (each a whole table) as the tables."""
+    state = {k: v.detach().cpu() for k, v in engram.state_dict().items()}
+    for k, shard in enumerate(getattr(engram, "row_shards", None) or []):
+        state[f"tables.{k}.weight"] = shard.detach().cpu()
+    return state
 
 
-def save_engram_weights(engram, path, layer=None, fmt=None, prefix="model.language_model.layers"):
-    """Write the engram in one of the formats load_engram_weights reads. fmt: "pt" (local names,
-    like micro_engram.pt), "safetensors" (one file), "safetensors_dir" (a folder with
-    micro_engram.safetensors) or "dcp" (a DCP folder); by default from the path's suffix (a path
-    without one is a DCP folder). With `layer`, tensors get full names (several engrams can
-    share one file); "safetensors_dir" and "dcp" need it, as model checkpoints have them."""
-    if fmt is None:
-        fmt = "pt" if path.endswith(".pt") else "safetensors" if path.endswith(".safetensors") else "dcp"
-    sd = engram_state(engram)
-    if layer is not None:
-        sd = {full_name(layer, k, prefix): v for k, v in sd.items()}
-    elif fmt in ("safetensors_dir", "dcp"):
-        raise ValueError(f"[micro_engram] a {fmt} engram checkpoint needs the decoder layer (full names)")
-    if fmt == "pt":
-        torch.save(sd, path)
-    elif fmt in ("safetensors", "safetensors_dir"):
-        from safetensors.torch import save_file
+_WRITERS = {}
 
-        if fmt == "safetensors_dir":
-            os.makedirs(path, exist_ok=True)
-            path = os.path.join(path, ENGRAM_FILE)
-        save_file({k: v.contiguous() for k, v in sd.items()}, path)
-    elif fmt == "dcp":
-        import torch.distributed.checkpoint as dcp
 
-        dcp.save(sd, checkpoint_id=path, no_dist=True)
-    else:
-        raise ValueError(f"[micro_engram] unknown weights format {fmt!r}")
+def _writer(fmt):
+    def register(fn):
+        _WRITERS[fmt] = fn
+        return fn
+
+    return register
+
+
+@_writer("pt")
+def _write_pt(state, path):
+    torch.save(state, path)
     return path
 
 
-# ----------------------------------------------------------------------------- configs
+@_writer("safetensors")
+def _write_safetensors(state, path):
+    from safetensors.torch import save_file
+
+    save_file({k: v.contiguous() for k, v in state.items()}, path)
+    return path
+
+
+@_writer("safetensors_dir")
+def _write_safetensors_dir(state, path):
+    os.makedirs(path, exist_ok=True)
+    return _write_safetensors(state, os.path.join(path, ENGRAM_FILE))
+
+
+@_writer("dcp")
+def _write_dcp(state, path):
+    import torch.distributed.checkpoint as dcp
+
+    dcp.save(state, checkpoint_id=path, no_dist=True)
+    return path
+
+
+def save_engram_weights(engram, path, layer=None, fmt=None, prefix="model.language_model.layers"):
+    """Write the engram where load_engram_weights (and the reference's loaders) read it back.
+    fmt: "pt", "safetensors", "safetensors_dir" (a folder with micro_engram.safetensors) or "dcp";
+    by default from the suffix of `path` (none: a DCP folder). With `layer` the tensors get full
+    names, so one file can hold several engrams; the two folder formats are model checkpoints and
+    need it. Returns the path written."""
+    if fmt is None:
+        fmt = {".pt": "pt", ".safetensors": "safetensors"}.get(os.path.splitext(path)[1], "dcp")
+    if fmt not in _WRITERS:
+        raise ValueError(f"[micro_engram] no writer for weights format {fmt!r} (have {sorted(_WRITERS)})")
+    state = engram_state(engram)
+    if layer is not None:
+        state = {full_name(layer, k, prefix): v for k, v in state.items()}
+    elif fmt in ("safetensors_dir", "dcp"):
+        raise ValueError(f"[micro_engram] the {fmt} format is a model checkpoint: give the decoder layer")
+    return _WRITERS[fmt](state, path)
+
+
+# ------------------------------------------------------------------------------ configs
 def norm_table_sizes(sizes):
-    """{order: rows or None} with integer orders (JSON keys are strings), or None
-    (weights.py:162-166)."""
+    """Per-order table sizes with integer orders (JSON object keys are strings) and 0 as None;
+    None when there are none."""
     if not sizes:
         return None
-    return {int(order): (int(rows) if rows else None) for order, rows in dict(sizes).items()}
+    return {int(order): int(rows) if rows else None for order, rows in dict(sizes).items()}
+
+
+def _relative_to(conf_path, target):
+    """`target` read relative to the folder of the config file (absolute paths unchanged)."""
+    if not target or os.path.isabs(target) or not conf_path:
+        return target or None
+    return os.path.join(os.path.dirname(os.path.abspath(conf_path)), target)
 
 
 def resolve_weights_path(conf, conf_path):
-    """The top-level "weights" of a config, relative to the config's folder, or None
-    (weights.py:143-150)."""
-    w = conf.get("weights")
-    if not w:
-        return None
-    return w if os.path.isabs(w) else os.path.join(os.path.dirname(os.path.abspath(conf_path)), w)
+    """The config's top-level "weights", relative to the config's folder, or None."""
+    return _relative_to(conf_path, conf.get("weights"))
+
+
+def _normalise(spec):
+    """Defaults of configs that predate a field: layer 0, orders (2, 3), the scalar gate, seed 0."""
+    spec["layer"] = int(spec.get("layer") or 0)
+    spec["orders"] = tuple(spec.get("orders") or (2, 3))
+    spec["table_sizes"] = norm_table_sizes(spec.get("table_sizes"))
+    spec["gate"] = spec.get("gate") or "scalar"
+    spec["seed"] = 0 if spec.get("seed") is None else int(spec["seed"])
+    return spec
 
 
 def engram_specs(conf, conf_path=None):
-    """One settings dict per engram of a micro_engram_config.json (weights.py:172-200): the
-    "engrams" list, or the single engram described at the top level by older configs. Each
-    entry inherits the top-level fields it leaves unset; layer defaults to 0, orders to (2, 3),
-    gate to "scalar" and seed to 0 (configs from before seeds were recorded); "weights" is
-    resolved against the config's folder. Two engrams in one layer are an error."""
-    top = {k: conf.get(k) for k in _SPEC_FIELDS}
-    entries = conf.get("engrams") or [{**top, "weights": conf.get("weights")}]
+    """Settings of each engram of a micro_engram_config.json: the entries of its "engrams" list,
+    each taking the top-level value of any setting it leaves unset, or -- in configs from before
+    several engrams -- one engram described by the top level itself. "weights" is per entry and
+    read relative to the config's folder. Raises if two engrams share a layer."""
+    shared = {k: conf.get(k) for k in SPEC_KEYS}
+    entries = conf.get("engrams")
+    if not entries:
+        entries = [dict(shared, weights=conf.get("weights"))]
     specs = []
     for entry in entries:
-        spec = dict(top)
-        spec.update({k: v for k, v in entry.items() if v is not None or k == "weights"})
-        spec["layer"] = int(spec.get("layer") or 0)
-        spec["orders"] = tuple(spec.get("orders") or (2, 3))
-        spec["table_sizes"] = norm_table_sizes(spec.get("table_sizes"))
-        spec["gate"] = spec.get("gate") or "scalar"
-        spec["seed"] = int(spec["seed"]) if spec.get("seed") is not None else 0
-        w = entry.get("weights")
-        if w and conf_path and not os.path.isabs(w):
-            w = os.path.join(os.path.dirname(os.path.abspath(conf_path)), w)
-        spec["weights"] = w or None
+        own = {k: v for k, v in entry.items() if v is not None}
+        spec = _normalise({**shared, **own})
+        spec["weights"] = _relative_to(conf_path, entry.get("weights"))
         specs.append(spec)
-    layers = [s["layer"] for s in specs]
-    if len(set(layers)) != len(layers):
-        raise ValueError(f"[micro_engram] two engrams in the same layer: {layers}")
+    layers = sorted(s["layer"] for s in specs)
+    if len(set(layers)) < len(layers):
+        raise ValueError(f"[micro_engram] the config puts more than one engram in a layer: layers {layers}")
     return specs
 
 
 def latest_checkpoint(folder):
-    """The newest complete checkpoint-N in `folder` (trainer_state.json is written last), or
-    None (weights.py:206-211)."""
-    best = None
-    for c in glob.glob(os.path.join(folder, "checkpoint-*")):
-        m = _CHECKPOINT_DIR.search(c)
-        if m and os.path.isfile(os.path.join(c, "trainer_state.json")):
-            if best is None or int(m.group(1)) > best[0]:
-                best = (int(m.group(1)), c)
-    return None if best is None else best[1]
+    """The checkpoint-N folder in `folder` with the largest N among the complete ones (the
+    trainer writes trainer_state.json last), or None."""
+    done = []
+    for sub in glob.glob(os.path.join(folder, "checkpoint-*")):
+        m = _CHECKPOINT.match(os.path.basename(sub))
+        if m and os.path.isfile(os.path.join(sub, "trainer_state.json")):
+            done.append((int(m.group(1)), sub))
+    return max(done)[1] if done else None
 
 
 def spec_for_layer(conf_path, layer):
-    """The settings of the engram at `layer` in the config at conf_path (weights.py:239-246)."""
+    """Settings of decoder `layer`'s engram in the config file conf_path."""
     with open(conf_path) as f:
-        specs = engram_specs(json.load(f), conf_path)
-    for spec in specs:
-        if spec["layer"] == layer:
-            return spec
-    raise ValueError(f"[micro_engram] {conf_path} has no engram at layer {layer} "
-                     f"(it has layers {[s['layer'] for s in specs]})")
+        specs = {s["layer"]: s for s in engram_specs(json.load(f), conf_path)}
+    if layer not in specs:
+        raise ValueError(f"[micro_engram] {conf_path} has no engram at layer {layer}; its engrams are at "
+                         f"layers {sorted(specs)}")
+    return specs[layer]
 
 
 def resolve_engram_source(path, layer):
-    """(weights path, settings or None) of the trained engram for decoder `layer`
-    (weights.py:214-236). `path`: a micro_engram_config.json, a folder holding one (a
-    checkpoint-N, an assembled model, or an output_dir whose newest checkpoint is used), or the
-    weights themselves."""
+    """(weights path, settings or None) of decoder `layer`'s trained engram, from
+      * a micro_engram_config.json file, or a folder that has one next to its weights;
+      * a training output folder: its newest complete checkpoint-N (settings from that
+        checkpoint's config, else the output folder's);
+      * the weights themselves (settings unknown: None)."""
     path = os.path.abspath(path)
-    conf_path = path if path.endswith(".json") else os.path.join(path, CONFIG_NAME)
-    if os.path.isdir(path) and not _is_dcp(path):
-        has_conf = os.path.isfile(conf_path)
-        has_weights = bool(glob.glob(os.path.join(path, "*.safetensors")))
-        ckpt = None if has_weights else latest_checkpoint(path)
-        if ckpt is not None:
-            weights, spec = resolve_engram_source(ckpt, layer)
-            if spec is None and has_conf:
-                spec = spec_for_layer(conf_path, layer)
+    config = path if path.endswith(".json") else os.path.join(path, CONFIG_NAME)
+    folder_of_weights = os.path.isdir(path) and not is_dcp_folder(path)
+    if folder_of_weights and not glob.glob(os.path.join(path, "*.safetensors")):
+        newest = latest_checkpoint(path)
+        if newest is not None:
+            weights, spec = resolve_engram_source(newest, layer)
+            if spec is None and os.path.isfile(config):
+                spec = spec_for_layer(config, layer)
             return weights, spec
-    if os.path.isfile(conf_path):
-        spec = spec_for_layer(conf_path, layer)
-        return spec["weights"] or os.path.dirname(conf_path), spec
+    if os.path.isfile(config):
+        spec = spec_for_layer(config, layer)
+        return (spec["weights"] or os.path.dirname(config)), spec
     return path, None
 
 
 def check_canon(canon, vocab_size):
-    """A token-merge map read from disk, validated (runconfig.py:91-100): 1-D of vocab_size ids
-    inside the vocabulary, and idempotent (canon[canon] == canon)."""
+    """A token-merge map read from disk, checked as the reference's config loader checks it
+    (runconfig.py:91-100): 1-D, vocab_size long, ids inside the vocabulary, idempotent
+    (canon[canon] == canon: a canonical id maps to itself). Returns it as int64."""
     if not torch.is_tensor(canon) or canon.dim() != 1 or canon.numel() != vocab_size:
-        raise ValueError(f"[micro_engram] canon file must be a 1-D tensor of length {vocab_size}")
+        raise ValueError(f"[micro_engram] a canon map is a 1-D tensor with one id per token: length "
+                         f"{vocab_size} expected")
     canon = canon.long()
-    if int(canon.min()) < 0 or int(canon.max()) >= vocab_size:
-        raise ValueError("[micro_engram] canon file has ids outside the vocabulary")
+    if canon.numel() and (int(canon.min()) < 0 or int(canon.max()) >= vocab_size):
+        raise ValueError(f"[micro_engram] the canon map points outside the vocabulary [0, {vocab_size})")
     if not torch.equal(canon[canon], canon):
-        raise ValueError("[micro_engram] canon map is not idempotent (a canonical id must map to itself)")
+        raise ValueError("[micro_engram] the canon map is not idempotent: some token maps to an id that "
+                         "is not its own canonical id")
     return canon
 
 
-# ----------------------------------------------------------------------------- base check
-_FP_PROJ = re.compile(r"^(.*\.layers\.)(\d+)\.(self_attn\.[qkvo]_proj|mlp\.(?:gate|up|down)_proj)\.weight$")
-_FP_ROWS = 64
-
-
-def _model_weight_files(model_dir):
-    index = os.path.join(model_dir, "model.safetensors.index.json")
-    if os.path.isfile(index):
-        with open(index) as f:
-            return {k: os.path.join(model_dir, v) for k, v in json.load(f)["weight_map"].items()}
-    from safetensors import safe_open
-
-    files = {}
-    for f in sorted(glob.glob(os.path.join(model_dir, "*.safetensors"))):
-        with safe_open(f, framework="pt", device="cpu") as fh:
-            files.update({k: f for k in fh.keys()})
-    return files
-
-
-def base_fingerprint(model_dir):
-    """16 hex digits identifying a base model's weights (weights.py:266-310): SHA-256 over the
-    first 64 rows of the token embedding and of the attention / MLP projections of the first,
-    middle and last decoder layer, each tagged by its role (not its name), dtype and shape. None
-    without safetensors weights."""
-    from safetensors import safe_open
-
-    if not os.path.isdir(model_dir):
-        return None
-    files = {k: f for k, f in _model_weight_files(model_dir).items()
-             if TAG not in k and "vision" not in k and "audio" not in k}
-    if not files:
-        return None
-    roles = {"embed": k for k in files if k.endswith("embed_tokens.weight")}
-    by_layer = {}
-    for k in files:
-        m = _FP_PROJ.match(k)
-        if m:
-            by_layer.setdefault(int(m.group(2)), {})[m.group(3)] = k
-    if by_layer:
-        ids = sorted(by_layer)
-        for where, i in (("first", ids[0]), ("middle", ids[len(ids) // 2]), ("last", ids[-1])):
-            roles.update({f"{where}.{r}": k for r, k in by_layer[i].items()})
-    if not roles:
-        return None
-    h = hashlib.sha256()
-    for role in sorted(roles):
-        k = roles[role]
-        with torch.device("cpu"), safe_open(files[k], framework="pt", device="cpu") as fh:
-            t = fh.get_slice(k)[:_FP_ROWS].contiguous().cpu()
-        h.update(role.encode())
-        h.update(str((t.dtype, tuple(t.shape))).encode())
-        h.update(t.view(torch.uint8).numpy().tobytes())
-    return h.hexdigest()[:16]
-
-
-def base_mismatch(conf, model_dir):
-    """A warning text when the engram was trained on other base weights, else None
-    (weights.py:313-328). It never raises: a failed check is reported as a warning."""
-    want = conf.get("base_fingerprint")
-    if not want:
-        return None
-    try:
-        have = base_fingerprint(model_dir)
-    except Exception as e:  # noqa: BLE001
-        return f"could not check which base weights this engram was trained on ({type(e).__name__}: {e})"
-    if have is None or have == want:
-        return None
-    return (f"this engram was trained on different base weights (trained on {conf.get('base_model', '?')}, "
-            f"fingerprint {want}; this model: {have}). It still loads, but it injects into hidden "
-            f"states it never saw: expect worse output unless this is really the same base.")
-
-
 def load_engram(path, layer, model_dim, vocab_size, device=None, dtype=None, pad_default=0):
-    """A MicroEngram for decoder `layer` rebuilt from a trained one at `path` (any form
-    resolve_engram_source takes): its settings (seed included, which fixes every hash address)
-    from the config, its tensors checked and loaded (check_loaded), the canon map validated.
-    Without a config the settings cannot be known and this raises."""
+    """A MicroEngram rebuilt from decoder `layer`'s trained engram at `path` (any form
+    resolve_engram_source accepts): settings, the seed among them (it fixes every hash
+    address), from the config; tensors loaded and checked against those settings; the canon map
+    validated. Without a config the settings are unknown, and this raises."""
     from .module import check_loaded, engram_from_spec
 
     weights, spec = resolve_engram_source(path, layer)
     if spec is None:
-        raise ValueError(f"[micro_engram] {path}: no {CONFIG_NAME} found, so the engram's settings "
-                         f"(sizes, orders, seed) are unknown")
-    sd = load_engram_weights(weights, layer=layer, need_layer=True)
-    canon = sd.get("canon")
-    if canon is not None:
-        canon = check_canon(canon, vocab_size)
-    eng = engram_from_spec(spec, model_dim, vocab_size, pad_default=pad_default, canon=canon)
-    check_loaded(eng, sd, weights)
-    return eng.to(device=device, dtype=dtype) if (device is not None or dtype is not None) else eng
+        raise ValueError(f"[micro_engram] found no {CONFIG_NAME} for {path}: the engram's sizes, orders "
+                         "and seed are unknown")
+    state = load_engram_weights(weights, layer=layer, need_layer=True)
+    canon = state.get("canon")
+    engram = engram_from_spec(spec, model_dim, vocab_size, pad_default=pad_default,
+                              canon=None if canon is None else check_canon(canon, vocab_size))
+    check_loaded(engram, state, weights)
+    if device is None and dtype is None:
+        return engram
+    return engram.to(device=device, dtype=dtype)

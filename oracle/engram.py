@@ -11,11 +11,16 @@ hash_ids                 micro_engram/module.py:183-205                   exact 
 hash_prev                micro_engram/module.py:207-226                   hash_prev == hash_ids
                                                                           (test_vllm_ids.py:68-83)
 lookup                   module.py:146-154, micro_engram_vllm/tp.py:20-39 numpy fancy indexing identity
-inject                   micro_engram/module.py:228-261                   closed forms (constant hidden
-                                                                          and key give s = +-sqrt(d));
-                                                                          value=0 no-op and keep-mask
-                                                                          cases of test_gate.py:24-27,
-                                                                          122-130
+inject                   micro_engram/module.py:228-261                   test_oracle_inject.py: value=0
+                                                                          no-op and keep mask
+                                                                          (test_gate.py:24-27, 122-130);
+                                                                          hidden 0 -> alpha 1/2 exactly;
+                                                                          constant hidden and key ->
+                                                                          closed-form s0 = sqrt(d) c c'
+                                                                          r_h r_k (fp32 eps visible);
+                                                                          scales multiply s0; the 1e-6
+                                                                          clamp; bf16 roundings of K and
+                                                                          of the add
 inject_backward          autograd of micro_engram/module.py:239-261       torch.autograd of inject on the
                          (closed form, float64)                           same inputs; finite differences
                                                                           of inject in float64
@@ -24,6 +29,11 @@ dedup                    micro_engram/rows.py:81, 117-118, 137-147        brute-
 philox4x32_10            Salmon et al. 2011 (Random123)                   published known-answer vectors
 stochastic_bf16          micro_engram/optim.py:33-44                      exhaustive 2^16-noise count;
                                                                           fp32 pass-through, inf kept
+clip_coef, clip          micro_engram/rows.py:208-233                     test_oracle_rows.py: norms of
+                                                                          known gradients; coef < 1
+                                                                          brings the norm to max_norm;
+                                                                          coef 1 leaves them bit-equal;
+                                                                          bf16 scaled by the bf16 coef
 sparse_adam_step         micro_engram/optim.py:65-133 (sparse branch)     == torch.optim.AdamW when |g| is
                                                                           uniform per row
                                                                           (test_optim.py:74-80); lazy
@@ -141,6 +151,32 @@ def hash_prev(ids, mults, orders, rows, canon, pad_id):
     return out
 
 
+def hash_ids_torch(input_ids, mults, orders, rows, canon, pad_id, position_ids=None):
+    """hash_ids as torch-CPU tensor ops, step for step as module.py:183-205 writes them (canon
+    after a clamp, left pad with the raw pad id, shifted views, the document-boundary mask, the
+    int64 sum of products, then % P % rows): the CPU baseline's hash. Returns int64 [n_tables,
+    B, T]."""
+    ids = torch.as_tensor(input_ids).long()
+    canon = torch.as_tensor(canon).long()
+    mults = torch.as_tensor(mults).long()
+    ids = canon[ids.clamp(0, canon.numel() - 1)]
+    T = ids.shape[-1]
+    width = max(orders)
+    padded = F.pad(ids, (width - 1, 0), value=pad_id)
+    shifted = [padded[:, width - 1 - i: width - 1 - i + T] for i in range(width)]
+    if position_ids is not None:
+        pos = torch.as_tensor(position_ids).long().expand_as(ids)
+        shifted = [s if i == 0 else torch.where(pos >= i, s, torch.full_like(s, pad_id))
+                   for i, s in enumerate(shifted)]
+    out = []
+    for k, n in enumerate(orders):
+        x = shifted[0] * mults[k, 0]
+        for i in range(1, n):
+            x = x + shifted[i] * mults[k, i]
+        out.append((x % PRIME) % int(rows[k]))
+    return torch.stack(out)
+
+
 def hash_bigint(tokens, mults_row, order, rows):
     """One n-gram row id in Python's arbitrary-precision integers: sum(tok_i * mult_i) % P % rows.
     Exact whenever the int64 sum does not wrap (|tokens| < 2^31)."""
@@ -255,6 +291,31 @@ def dedup(keys, grads):
     acc = np.zeros((uniq.size,) + grads.shape[1:], dtype=np.float32)
     np.add.at(acc, inv, grads)  # unbuffered, in index order: ((0 + g_a) + g_b) + ...
     return uniq, inv.astype(np.int64), acc
+
+
+# -------------------------------------------------------------------------------------- clip
+def clip_coef(norm, max_norm):
+    """The clipping coefficient of RowTables.clip (rows.py:221-226) from the fp32 norm, in
+    fp32 torch-CPU ops as the reference writes them: (max_norm / (norm + 1e-6)).clamp(max=1.0)
+    -- the division is Tensor.__rtruediv__, a reciprocal then a product."""
+    norm = torch.as_tensor(norm, dtype=torch.float32)
+    return (max_norm / (norm + 1e-6)).clamp(max=1.0)
+
+
+def clip(grads, max_norm):
+    """RowTables.clip (rows.py:208-233) on a list of gradients (dense tables' p.grad in any
+    float dtype, or sparse_grad fp32 sums): the global norm of all of them, and each scaled in
+    place by the coefficient when max_norm > 0 (fp32 sums by the fp32 coefficient, other
+    dtypes by the coefficient cast to theirs). Returns the norm as a Python float."""
+    sq = torch.zeros((), dtype=torch.float32)
+    for g in grads:
+        sq += g.float().pow(2).sum()
+    norm = sq.sqrt()
+    if max_norm and max_norm > 0:
+        coef = (max_norm / (norm + 1e-6)).clamp(max=1.0)
+        for g in grads:
+            g.mul_(coef.to(g.dtype))
+    return float(norm)
 
 
 # ----------------------------------------------------------------------------- random numbers

@@ -286,3 +286,27 @@ def test_serving_decode_step_sampled():
     assert_close_out(out, ref, hidden, torch.bfloat16)
     del eng
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_forward_after_optimizer_step_sees_new_weights(dtype):
+    """A no-grad forward, a LazyAdamW step on the key / value weights (the optimizer writes
+    through raw pointers), then a second forward: it must use the updated weights (both gate
+    paths), and equal the oracle on them."""
+    from micro_engram_fork_amd.optim import LazyAdamW
+
+    torch.manual_seed(3)
+    eng = _make(dtype, d=64, dim=8, heads=2)
+    ids = torch.randint(5, 1000, (1, 40), device=DEV)
+    hidden = torch.randn(1, 40, 64).to(dtype).to(DEV)
+    with torch.no_grad():
+        before = eng(hidden, ids)
+    opt = LazyAdamW([eng.key.weight, eng.value.weight], lr=0.05, lazy=False, seed=1)
+    eng.key.weight.grad = torch.randn_like(eng.key.weight)
+    eng.value.weight.grad = torch.randn_like(eng.value.weight)
+    opt.step()
+    with torch.no_grad():
+        after = eng(hidden, ids)
+    assert not torch.equal(before, after)
+    ref, _ = _oracle_forward(eng, hidden, ids)
+    assert_close_out(after, ref.reshape(after.shape), hidden, dtype)

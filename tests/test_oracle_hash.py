@@ -191,3 +191,16 @@ def test_golden_fixture():
     prev = oracle.hash_prev(f["prev_ids"], f["mults"], list(f["orders"]), list(f["rows"]),
                             f["canon"], int(f["pad_id"]))
     assert np.array_equal(prev, f["prev_idx"])
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_torch_restatement_equals_c_oracle(seed):
+    # the CPU baseline's torch-op hash gives the C oracle's row ids bit for bit (big-integer
+    # brute force pins the C oracle above)
+    rng = np.random.Generator(np.random.PCG64(100 + seed))
+    ids, pos, canon, mults, orders, rows = _random_case(
+        rng, 2, 41, 700, orders_heads=((2, 3), (3, 2), (4, 1)), with_pos=seed % 2 == 0)
+    pad = int(rng.integers(0, 700))
+    want = oracle.hash_ids(ids, mults, orders, rows, canon, pad, position_ids=pos)
+    got = oracle.hash_ids_torch(ids, mults, orders, rows, canon, pad, position_ids=pos)
+    assert np.array_equal(got.numpy(), want)

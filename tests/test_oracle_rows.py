@@ -193,3 +193,54 @@ def test_bf16_second_moment_freeze_vs_stochastic_rounding():
     assert results["plain"] < 0.5
     assert abs(results["sr"] - 1) < 0.02
     assert abs(results["rowwise"] - 1) < 1e-4
+
+
+# ------------------------------------------------------------------------------------- clip
+def test_clip_norm_of_known_gradients():
+    """rows.py:214-223: the norm over every gradient, dense and sparse: 3-4-12 gives 13."""
+    a = torch.tensor([[3.0, 0.0]])
+    b = torch.tensor([[4.0], [12.0]])
+    assert oracle.clip([a, b], 0.0) == 13.0
+    assert torch.equal(a, torch.tensor([[3.0, 0.0]]))  # max_norm 0: no scaling
+
+
+def test_clip_scales_to_max_norm():
+    """coef < 1 scales the gradients so that their norm becomes max_norm (within fp32)."""
+    g = torch.Generator().manual_seed(0)
+    grads = [torch.randn(50, 8, generator=g) * 3, torch.randn(7, 8, generator=g)]
+    norm = oracle.clip(grads, 2.5)
+    assert norm > 2.5
+    after = float(torch.cat([x.reshape(-1) for x in grads]).double().pow(2).sum().sqrt())
+    assert after == pytest.approx(2.5, rel=1e-6)
+
+
+def test_clip_below_max_norm_is_identity():
+    """coef = min(max_norm / (norm + 1e-6), 1) = 1 exactly: the gradients stay bit-equal."""
+    g = torch.Generator().manual_seed(1)
+    grads = [torch.randn(20, 4, generator=g) * 1e-3, (torch.randn(5, 4, generator=g) * 1e-3).bfloat16()]
+    before = [x.clone() for x in grads]
+    oracle.clip(grads, 10.0)
+    for x, y in zip(grads, before):
+        assert torch.equal(x, y)
+
+
+def test_clip_bf16_uses_rounded_coef():
+    """A bf16 gradient is scaled by the coefficient rounded to bf16 (p.grad.mul_(coef.to(bf16))):
+    with norm 3 and max_norm 1 the coefficient 1/3 rounds to 0.333984375 in bf16, so 3.0
+    becomes round_bf16(3 x 0.333984375) = 1.0 (1.001953125 is nearer 1.0 than 1.0078125), while fp32
+    sums are scaled by the fp32 coefficient."""
+    dense = torch.tensor([3.0], dtype=torch.bfloat16)
+    sparse = torch.tensor([[0.0]])
+    oracle.clip([dense, sparse], 1.0)
+    assert float(torch.tensor(1 / 3).bfloat16()) == 0.333984375
+    assert float(dense) == 1.0
+    f32 = torch.tensor([3.0])
+    oracle.clip([f32], 1.0)
+    assert float(f32) == pytest.approx(1.0, rel=1e-6) and float(f32) != 1.001953125
+
+
+def test_clip_coef_matches_clip():
+    c = oracle.clip_coef(torch.tensor(200.0).sqrt(), 1.0)
+    x = torch.tensor([10.0, 10.0])  # norm^2 = 200
+    oracle.clip([x], 1.0)
+    assert torch.equal(x, torch.full((2,), 10.0) * c)

@@ -296,21 +296,98 @@ def test_row_lookup_backward_sparse_grads():
         assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), acc.view(np.int32))
 
 
-def test_row_tables_clip_scales_next_step():
-    eng = MicroEngram(model_dim=16, table_size=64, engram_dim=8, num_heads=1, orders=(2,), vocab_size=50)
-    shards = eng.shard_rows(0, 1, device=DEV)
-    rt = me_rows.RowTables([("x.", eng)], lr=1e-1, lazy=True, rowwise=True, sparse_grads=True,
-                           stochastic_rounding=False, seed=0)
-    before = shards[0].detach().clone()
-    rows = torch.tensor([1, 5, 9], device=DEV)
-    g = torch.full((3, 8), 3.0, device=DEV)
-    me_rows.add_sparse_grad(shards[0], rows, g)
+def _clip_engram(dtype, sparse):
+    eng = MicroEngram(model_dim=16, table_size=64, engram_dim=8, num_heads=2, orders=(2,), vocab_size=50,
+                      seed=4)
+    shards = eng.shard_rows(0, 1, device=DEV, dtype=dtype)
+    rt = me_rows.RowTables([("x.", eng)], lr=5e-3, lazy=True, rowwise=True, sparse_grads=sparse,
+                           stochastic_rounding=True, seed=77)
+    return eng, shards, rt
+
+
+def _oracle_step(init, rows, g, step, table, seed=77):
+    p_ref = init.clone()
+    m_ref = torch.zeros_like(p_ref)
+    v_ref = torch.zeros(p_ref.shape[0])
+
+    def noise(r, which):
+        return torch.from_numpy(oracle.sr_noise(seed, step, table, r.numpy(), init.shape[1], which))
+
+    oracle.sparse_adam_step(p_ref, m_ref, v_ref, rows, g, step, 5e-3, stochastic_rounding=True, noise=noise)
+    return p_ref, m_ref, v_ref
+
+
+def test_row_tables_clip_sparse_in_place_then_step():
+    """RowTables.clip with coef < 1 (rows.py:208-233): the fp32 sparse sums are scaled in place
+    by the fp32 coefficient -- bit-equal to the oracle's scaling given the same norm, the norm
+    itself within 1e-6 of the oracle's (another summation order) -- and the next step equals the
+    oracle's clip followed by sparse_adam_step with the same rounding noise."""
+    eng, shards, rt = _clip_engram(torch.bfloat16, sparse=True)
+    init = [s.detach().cpu().clone() for s in shards]
+    g = torch.Generator().manual_seed(11)
+    rows = [torch.tensor([1, 5, 9, 40]), torch.tensor([0, 2, 63])]
+    sums = [torch.randn(r.numel(), 8, generator=g) * 2.0 for r in rows]
+    for s, r, x in zip(shards, rows, sums):
+        me_rows.add_sparse_grad(s, r.to(DEV), x.to(DEV))
     norm = rt.clip(1.0)
-    assert abs(norm - (9 * 24) ** 0.5) < 1e-4
-    rt.step(1e-1)
-    assert shards[0].sparse_grad is None
-    moved = (shards[0].detach() - before).abs().sum(1)
-    assert (moved[[1, 5, 9]] > 0).all() and moved.sum() == moved[[1, 5, 9]].sum()
+    ref_sums = [x.clone() for x in sums]
+    ref_norm = oracle.clip(ref_sums, 1.0)
+    assert norm == pytest.approx(ref_norm, rel=1e-6) and norm > 1.0
+    coef = oracle.clip_coef(norm, 1.0)  # the coefficient of the GPU's own norm
+    for s, x in zip(shards, sums):
+        assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), (x * coef).numpy().view(np.int32))
+    scaled = [s.sparse_grad[1].cpu().clone() for s in shards]
+    rt.step(5e-3)
+    for k, s in enumerate(shards):
+        p_ref, m_ref, v_ref = _oracle_step(init[k], rows[k], scaled[k], 1, k)
+        st = rt.optimizer.state[s]
+        _assert_bf16_close(s.detach().cpu(), p_ref)
+        _assert_bf16_close(st["exp_avg"].cpu(), m_ref)
+        assert torch.allclose(st["exp_avg_sq"].cpu(), v_ref, rtol=1e-6, atol=0)
+        assert s.sparse_grad is None
+
+
+def test_row_tables_clip_dense_bf16_in_place_then_step():
+    """Dense bf16 table gradients: p.grad.mul_(coef.to(bf16)) in place, bit-equal to the
+    oracle's given the same norm; then the lazy step over every row (all-zero rows skipped)."""
+    eng, shards, rt = _clip_engram(torch.bfloat16, sparse=False)
+    init = [s.detach().cpu().clone() for s in shards]
+    g = torch.Generator().manual_seed(12)
+    grads = []
+    for s in shards:
+        x = torch.zeros(s.shape)
+        x[torch.randperm(s.shape[0], generator=g)[:10]] = torch.randn(10, 8, generator=g) * 3.0
+        grads.append(x.bfloat16())
+        s.grad = grads[-1].to(DEV)
+    norm = rt.clip(0.5)
+    ref = [x.clone() for x in grads]
+    ref_norm = oracle.clip(ref, 0.5)
+    assert norm == pytest.approx(ref_norm, rel=1e-6) and norm > 0.5
+    coef = oracle.clip_coef(norm, 0.5).to(torch.bfloat16)
+    for s, x in zip(shards, grads):
+        want = (x * coef)  # bf16 * bf16: fp32 product rounded to bf16
+        assert torch.equal(s.grad.cpu().view(torch.int16), want.view(torch.int16))
+    scaled = [s.grad.cpu().float() for s in shards]
+    rt.step(5e-3)
+    for k, s in enumerate(shards):
+        p_ref, m_ref, v_ref = _oracle_step(init[k], torch.arange(s.shape[0]), scaled[k], 1, k)
+        _assert_bf16_close(s.detach().cpu(), p_ref)
+
+
+def test_row_tables_clip_then_zero_grad_leaves_nothing():
+    """A clip without a step, then zero_grad: the next step sees only its own gradients."""
+    eng, shards, rt = _clip_engram(torch.bfloat16, sparse=True)
+    init = [s.detach().cpu().clone() for s in shards]
+    me_rows.add_sparse_grad(shards[0], torch.tensor([3], device=DEV), torch.full((1, 8), 50.0, device=DEV))
+    rt.clip(1e-3)
+    rt.zero_grad()
+    assert all(s.sparse_grad is None for s in shards)
+    x = torch.full((1, 8), 1e-3)
+    me_rows.add_sparse_grad(shards[1], torch.tensor([7], device=DEV), x.to(DEV))
+    rt.step(5e-3)
+    assert torch.equal(shards[0].detach().cpu(), init[0])  # untouched
+    p_ref, _, _ = _oracle_step(init[1], torch.tensor([7]), x, 1, 1)
+    _assert_bf16_close(shards[1].detach().cpu(), p_ref)
 
 
 # ------------------------------------------------------------ the sparse-update workload

@@ -1,10 +1,10 @@
 """On-disk formats on the CPU: every format the engram can be saved in reads back into an equal
 engram; tensor names with and without decoder layers; micro_engram_config.json parsing; the
-token-merge map check; the base-model fingerprint; row-table checkpoints with optimizer state.
+token-merge map check; row-table checkpoints with optimizer state.
 
 Modelled on the reference's own checks: test_rows.py:192-263 (DCP save/load, optimizer state,
 lazy <-> rowwise conversion, resume from a checkpoint without row sharding), test_multi.py:146-323
-(configs, several engrams, shared files, fingerprints) and runconfig.py:91-100 (canon).
+(configs, several engrams, shared files) and runconfig.py:91-100 (canon).
 """
 import json
 import os
@@ -142,7 +142,7 @@ def test_engram_specs_forms():
     assert b["layer"] == 29 and b["seed"] == 290203 and b["orders"] == (2, 3, 4)
     assert b["table_sizes"] == {2: 5, 3: 7, 4: None} and b["weights"] is None
     assert W.default_seed(29) == 290203
-    with pytest.raises(ValueError, match="same layer"):
+    with pytest.raises(ValueError, match="more than one engram in a layer"):
         W.engram_specs({"engrams": [{"layer": 2}, {"layer": 2}]})
     assert W.norm_table_sizes(None) is None
 
@@ -185,35 +185,6 @@ def test_check_canon():
     chain[3] = 1  # 7 -> 3 -> 1: not idempotent
     with pytest.raises(ValueError, match="idempotent"):
         W.check_canon(chain, 50)
-
-
-def test_base_fingerprint(tmp_path):
-    from safetensors.torch import save_file
-
-    g = torch.Generator().manual_seed(0)
-    base = {"model.embed_tokens.weight": torch.randn(80, 8, generator=g)}
-    for i in range(4):
-        for proj in ("self_attn.q_proj", "mlp.up_proj"):
-            base[f"model.layers.{i}.{proj}.weight"] = torch.randn(70, 8, generator=g)
-    a, b = tmp_path / "a", tmp_path / "b"
-    for d in (a, b):
-        os.makedirs(d)
-    save_file(base, str(a / "model.safetensors"))
-    # the same weights as a multimodal checkpoint with another naming, plus an engram tensor
-    renamed = {k.replace("model.", "model.language_model.", 1): v for k, v in base.items()}
-    renamed["model.language_model.layers.0.micro_engram.tables.0.weight"] = torch.zeros(3, 3)
-    save_file(renamed, str(b / "model.safetensors"))
-    fa, fb = W.base_fingerprint(str(a)), W.base_fingerprint(str(b))
-    assert fa is not None and len(fa) == 16 and fa == fb
-    base["model.layers.3.mlp.up_proj.weight"][0, 0] += 1  # last layer: part of the fingerprint
-    c = tmp_path / "c"
-    os.makedirs(c)
-    save_file(base, str(c / "model.safetensors"))
-    assert W.base_fingerprint(str(c)) != fa
-    assert W.base_mismatch({"base_fingerprint": fa}, str(a)) is None
-    assert "different base weights" in W.base_mismatch({"base_fingerprint": fa}, str(c))
-    assert W.base_mismatch({}, str(c)) is None
-    assert W.base_fingerprint(str(tmp_path / "nothing")) is None
 
 
 def _rows_engram(seed=3, requires_grad=True):
@@ -306,5 +277,5 @@ def test_row_tables_load_errors_and_plain_checkpoint(tmp_path):
     folder = str(tmp_path / "l3")
     dcp.save({"model.layers.3.micro_engram." + k: v for k, v in eng.state_dict().items()},
              checkpoint_id=folder, no_dist=True)
-    with pytest.raises(ValueError, match="has no tables.0.weight"):
+    with pytest.raises(ValueError, match="holds no tables.0.weight"):
         RowTables([("model.language_model.layers.9.micro_engram.", _rows_engram())], lazy=True).load(folder)
