@@ -169,6 +169,24 @@ int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n, int64_t mo
                      void *stream);
 
 /*
+ * me_gate_residual_noalloc -- me_gate_residual without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops that forbid
+ * allocation). It has no counterpart in the reference. Same arguments and results as
+ * me_gate_residual, the same kernels; the workspace is a static 4 MiB device array of the
+ * library, one per GPU, held until the process ends. It allocates nothing: n tokens of model_dim
+ * need (3 ceil(model_dim / 224) + 1) * 4 * n bytes of it (at most 14,364 tokens at model dim
+ * 5376); larger calls return ME_ERR_INVALID and launch nothing. The current device must be the
+ * one the tensors and the stream belong to. Calls that overlap on one GPU share the array and
+ * race: serialise them (one stream, or events).
+ */
+int me_gate_residual_noalloc(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                             const void *mem, int64_t mem_dim, const void *w_key,
+                             const void *w_value, int dtype, const void *q_scale_delta,
+                             const void *k_scale_delta, int scale_dtype, int gate_mode,
+                             const uint8_t *keep, void *out, float *alpha_out, float *row_stats,
+                             void *stream);
+
+/*
  * me_gate_rows -- the gate and residual add of me_gate_residual from key and value projections
  * computed elsewhere (few-token batches, where one GEMM of the memory vectors against the
  * stacked [W_K; W_V] on the library BLAS fills the part and me_gate_residual's 256-token tiles

@@ -31,6 +31,8 @@ SIGNATURES = {
     "me_gate_residual": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_int,
                          c_ptr, c_ptr, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_size,
                          c_ptr],
+    "me_gate_residual_noalloc": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_int,
+                                 c_ptr, c_ptr, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
     "me_gate_rows": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr, c_int,
                      c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
     "me_gate_backward_workspace_size": [c_i64, c_i64, ctypes.POINTER(c_size)],

@@ -41,6 +41,7 @@
 // of 16x16x32 MFMAs (gate224_kernel: whole rounds of tiles on the Gemma-scale shape).
 #include "me_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace me {
@@ -1347,6 +1348,77 @@ extern "C" int me_gate_residual(const void *hidden, int hidden_dtype, int64_t n,
     if (hidden_dtype == ME_BF16) ME_GATE_LAUNCH(float, uint16_t);
     ME_GATE_LAUNCH(float, float);
 #undef ME_GATE_LAUNCH
+}
+
+// ---- the allocation-free gate -----------------------------------------------------------------
+// me_gate_residual_noalloc runs me_gate_residual with its workspace (the per-(column tile, token)
+// partial sums and the per-token gates, fully written before they are read, so nothing needs
+// clearing) in this file-scope device array instead of caller memory. Every GPU the library
+// runs on holds its own copy until the process ends; its address on a device comes from
+// hipGetSymbolAddress, asked once per device with that device current. Calls that overlap on
+// one GPU share the array and race.
+constexpr size_t kScratchBytes = size_t{4} << 20;  // 4 MiB: 14,364 tokens at model dim 5376
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace me {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_on[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device.
+int scratch_on_current_device(void **ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error("me_gate_residual_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+        return ME_ERR_HIP;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error("me_gate_residual_noalloc: device %d beyond the %d this library tracks", dev, kMaxDevices);
+        return ME_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_on[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error("me_gate_residual_noalloc: no address for the scratch array on device %d: %s", dev,
+                      hipGetErrorString(e));
+            return ME_ERR_HIP;
+        }
+        g_scratch_on[dev] = p;
+    }
+    *ptr = g_scratch_on[dev];
+    return ME_OK;
+}
+}  // namespace
+}  // namespace me
+
+extern "C" int me_gate_residual_noalloc(const void *hidden, int hidden_dtype, int64_t n,
+                                        int64_t model_dim, const void *mem, int64_t mem_dim,
+                                        const void *w_key, const void *w_value, int dtype,
+                                        const void *q_scale_delta, const void *k_scale_delta,
+                                        int scale_dtype, int gate_mode, const uint8_t *keep,
+                                        void *out, float *alpha_out, float *row_stats,
+                                        void *stream) {
+    ME_CHECK_ARG(n >= 0 && model_dim >= 1, "bad shape n=%lld d=%lld", (long long)n, (long long)model_dim);
+    if (n == 0) return ME_OK;
+    const size_t need = workspace_bytes(n, model_dim);
+    if (need > kScratchBytes) {
+        set_error("me_gate_residual_noalloc: %lld tokens of model dim %lld need %zu bytes of scratch; the "
+                  "static scratch holds %zu (at most %lld tokens at this model dim): use me_gate_residual "
+                  "with a workspace",
+                  (long long)n, (long long)model_dim, need, kScratchBytes,
+                  (long long)(kScratchBytes / workspace_bytes(1, model_dim)));
+        return ME_ERR_INVALID;
+    }
+    void *ws = nullptr;
+    const int st = scratch_on_current_device(&ws);
+    if (st != ME_OK) return st;
+    return me_gate_residual(hidden, hidden_dtype, n, model_dim, mem, mem_dim, w_key, w_value, dtype,
+                            q_scale_delta, k_scale_delta, scale_dtype, gate_mode, keep, out, alpha_out,
+                            row_stats, ws, kScratchBytes, stream);
 }
 
 extern "C" int me_gate_backward_workspace_size(int64_t n, int64_t model_dim, size_t *bytes) {
