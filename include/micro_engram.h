@@ -187,11 +187,27 @@ int me_gate_residual_noalloc(const void *hidden, int hidden_dtype, int64_t n, in
                              void *stream);
 
 /*
+ * me_kv_proj -- the key and value projections of the memory vectors for few tokens: the two
+ * nn.Linear calls of MicroEngram.inject (micro_engram/module.py:245, 254), in the engram dtype
+ * with fp32 accumulation, written side by side for me_gate_rows:
+ *
+ *   kv[i][j] = round(sum_m mem[i][m] w_key[j][m]),  kv[i][d + j] = round(sum_m mem[i][m] w_value[j][m])
+ *
+ *   mem       [n, mem_dim] of dtype (ME_BF16 / ME_F32); w_key, w_value [model_dim, mem_dim]
+ *   kv        [n, 2 model_dim] of dtype
+ * model_dim a multiple of 8, mem_dim * element size a multiple of 16 bytes, every tensor
+ * 16-byte aligned, mem and each weight under 2 GiB. Meant for batches up to a few thousand
+ * tokens (a serving decode step); larger ones belong to me_gate_residual.
+ */
+int me_kv_proj(const void *mem, int64_t n, int64_t mem_dim, const void *w_key, const void *w_value,
+               int64_t model_dim, int dtype, void *kv, void *stream);
+
+/*
  * me_gate_rows -- the gate and residual add of me_gate_residual from key and value projections
- * computed elsewhere (few-token batches, where one GEMM of the memory vectors against the
- * stacked [W_K; W_V] on the library BLAS fills the part and me_gate_residual's 256-token tiles
- * would not). Replaces the rest of MicroEngram.inject after the two nn.Linear calls
- * (micro_engram/module.py:240-261), with the same arithmetic as me_gate_residual:
+ * computed elsewhere (few-token batches: me_kv_proj's output, where me_gate_residual's
+ * 256-token tiles would leave most of the part idle). Replaces the rest of
+ * MicroEngram.inject after the two nn.Linear calls (micro_engram/module.py:240-261), with the
+ * same arithmetic as me_gate_residual:
  *
  *   h = rms_norm(hidden) [* (1 + q_scale_delta)], k = rms_norm(K) [* (1 + k_scale_delta)]
  *   s = sum(h k) / sqrt(model_dim); ME_GATE_SCALAR_SQRT: s = sign(s) sqrt(max(|s|, 1e-6))

@@ -33,6 +33,7 @@ SIGNATURES = {
                          c_ptr],
     "me_gate_residual_noalloc": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_int,
                                  c_ptr, c_ptr, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
+    "me_kv_proj": [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr],
     "me_gate_rows": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr, c_int,
                      c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
     "me_gate_backward_workspace_size": [c_i64, c_i64, ctypes.POINTER(c_size)],
@@ -64,7 +65,7 @@ class EngramLibError(RuntimeError):
 
 
 def lib_path():
-    return os.environ.get("MICRO_ENGRAM_AMD_LIB", LIB_PATH)
+    return os.environ.get("MICRO_ENGRAM_AMD_LIB") or LIB_PATH
 
 
 def load():

@@ -241,14 +241,12 @@ class MicroEngram(nn.Module):
     def __getstate__(self):
         state = self.__dict__.copy()
         state["_canon_state"] = None  # a weakref does not copy; the copy decides again
-        state.pop("_kv_cache", None)  # rebuilt from the copy's own weights
         return state
 
     def _apply(self, fn, *args, **kwargs):
         # .to() / .cuda() give the buffer a new tensor with the same values: keep the decision
         st = self._canon_state
         known = st is not None and st[0]() is self.canon and st[1] == self.canon._version
-        self.__dict__.pop("_kv_cache", None)  # stacked weights of the old device / dtype
         out = super()._apply(fn, *args, **kwargs)
         if known:
             self._canon_state = (weakref.ref(self.canon), self.canon._version, st[2])
@@ -365,9 +363,10 @@ class MicroEngram(nn.Module):
         q = self.q_scale.detach() if sqrt else None
         k = self.k_scale.detach() if sqrt else None
         n_tok = hidden.numel() // hidden.shape[-1]
-        if (n_tok <= self.few_tokens_max and hidden.shape[-1] % 8 == 0
-                and not torch.compiler.is_compiling()):
-            outs = ops.gate_residual_rows(hidden, mem, self._kv_weight(), q, k, mode, keep, self.training)
+        limit = self.few_tokens_max if mem.dtype == torch.bfloat16 else self.few_tokens_max_fp32
+        if n_tok <= limit:
+            outs = ops.gate_residual_rows(hidden, mem, self.key.weight.detach(), self.value.weight.detach(),
+                                          q, k, mode, keep, self.training)
         else:
             outs = ops.gate_residual(hidden, mem, self.key.weight.detach(), self.value.weight.detach(),
                                      q, k, mode, keep, self.training)
@@ -375,24 +374,16 @@ class MicroEngram(nn.Module):
             self._record_gate(outs[1])
         return outs[0]
 
-    # Token counts up to which the gate without gradients runs the two projections as one
-    # library GEMM against the stacked [W_K; W_V] plus the row kernel (me_gate_rows) instead of
-    # the fused kernel, whose 256-token tiles come in whole rounds of the CUs and leave many of
-    # them idle below the last round (measured on MI355X, model dim 5376, memory dim 1536:
-    # 512 tokens ~30 us against ~83 us, 4096 ~147 against ~186, 6144 ~227 against ~278; at
-    # 8192 the fused kernel is ahead, ~299 against ~305).
-    few_tokens_max = 6144
-
-    def _kv_weight(self):
-        """[W_K; W_V] ([2d, M]) stacked once and kept while neither weight changes (same
-        tensors, same version counters: in-place updates and load_state_dict move them)."""
-        wk, wv = self.key.weight, self.value.weight
-        key = (wk.data_ptr(), wk._version, wv.data_ptr(), wv._version, wk.dtype, wk.device)
-        cached = self.__dict__.get("_kv_cache")
-        if cached is None or cached[0] != key:
-            cached = (key, torch.cat([wk.detach(), wv.detach()], 0))
-            self.__dict__["_kv_cache"] = cached
-        return cached[1]
+    # Token counts up to which the gate without gradients runs the key and value projections
+    # in the few-token kernel (me_kv_proj) and the gate in the row kernel (me_gate_rows) instead
+    # of the fused kernel, whose 256-token tiles come in whole rounds of the CUs and leave many
+    # of them idle below the last round. Measured on MI355X (model dim 5376, memory dim 1536,
+    # bf16): 256 tokens 33 us against 73, 1024 tokens 61 against 74, 1536 tokens 88 against 76.
+    # fp32 engrams: the fused kernel's fp32 tiles are 256 x 256 on 32x32x2 MFMAs, so a 2048-token
+    # batch (model dim 1024) gives it 32 tiles per pass (538 us) and the few-token path (83 us for
+    # the projection) stays ahead far longer.
+    few_tokens_max = 1024
+    few_tokens_max_fp32 = 16384
 
     def inject(self, hidden, idx, keep=None):
         """hidden + gated memory of the rows `idx` (module.py:228-261); keep: optional [N] bool,

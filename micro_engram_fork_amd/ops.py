@@ -317,21 +317,48 @@ def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep
     return res
 
 
+@torch.library.custom_op("micro_engram_amd::kv_proj", mutates_args=())
+def kv_proj(mem: torch.Tensor, w_key: torch.Tensor, w_value: torch.Tensor) -> torch.Tensor:
+    """[K | V] [N, 2d] in mem's dtype: the key and value nn.Linear outputs of
+    MicroEngram.inject (module.py:245, 254) for few tokens, in one hand-written MFMA kernel
+    (me_kv_proj). mem [N, M]; w_key, w_value [d, M] (nn.Linear layout)."""
+    dev = require_gpu(mem, w_key, w_value)
+    if mem.dim() != 2 or w_key.dim() != 2 or w_key.shape != w_value.shape or w_key.shape[1] != mem.shape[1]:
+        raise ValueError(f"[micro_engram] kv_proj: mem {tuple(mem.shape)} and weights {tuple(w_key.shape)}/"
+                         f"{tuple(w_value.shape)} do not fit")
+    if not (mem.dtype == w_key.dtype == w_value.dtype):
+        raise ValueError("[micro_engram] kv_proj: mem and the weights must share one dtype")
+    mem, w_key, w_value = (t.contiguous() for t in (mem, w_key, w_value))
+    mem, w_key, w_value = (t if _aligned(t) else t.clone() for t in (mem, w_key, w_value))
+    N, M = mem.shape
+    d = w_key.shape[0]
+    kv = torch.empty((N, 2 * d), dtype=mem.dtype, device=dev)
+    call("me_kv_proj", mem.data_ptr(), N, M, w_key.data_ptr(), w_value.data_ptr(), d, dtype_code(mem),
+         kv.data_ptr(), stream_of(dev))
+    return kv
+
+
+@kv_proj.register_fake
+def _(mem, w_key, w_value):
+    return mem.new_empty((mem.shape[0], 2 * w_key.shape[0]))
+
+
 @torch.library.custom_op("micro_engram_amd::gate_residual_rows", mutates_args=())
-def gate_residual_rows(hidden: torch.Tensor, mem: torch.Tensor, w_kv: torch.Tensor,
-                       q_scale_delta: Optional[torch.Tensor], k_scale_delta: Optional[torch.Tensor],
-                       gate_mode: int, keep: Optional[torch.Tensor], with_alpha: bool,
+def gate_residual_rows(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
+                       w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
+                       k_scale_delta: Optional[torch.Tensor], gate_mode: int,
+                       keep: Optional[torch.Tensor], with_alpha: bool,
                        with_stats: bool = False) -> List[torch.Tensor]:
-    """gate_residual for few tokens: [K | V] = mem @ w_kv^T as one GEMM on the library BLAS
-    (w_kv = [W_K; W_V], [2d, M]; K and V rounded to mem's dtype, as the two nn.Linear calls of
-    module.py:245, 254 give them), then the gate and residual add in me_gate_rows."""
-    dev = require_gpu(hidden, mem, w_kv, q_scale_delta, k_scale_delta, keep)
-    d = hidden.shape[-1]
-    if w_kv.dim() != 2 or w_kv.shape[0] != 2 * d:
-        raise ValueError(f"[micro_engram] stacked weight {tuple(w_kv.shape)} is not [2 * {d}, M]")
-    x, mem, _wk, _wv, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M = \
-        _gate_operands(hidden, mem, w_kv[:d], w_kv[d:], q_scale_delta, k_scale_delta, gate_mode, keep)
-    kv = torch.mm(mem, w_kv.t())
+    """gate_residual for few tokens: [K | V] from me_kv_proj (K and V rounded to mem's dtype, as
+    the two nn.Linear calls of module.py:245, 254 give them), then the gate and the residual add
+    in me_gate_rows."""
+    dev = require_gpu(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, keep)
+    x, mem, w_key, w_value, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M = \
+        _gate_operands(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep)
+    kv = torch.empty((N, 2 * d), dtype=mem.dtype, device=dev)
+    if N:
+        call("me_kv_proj", mem.data_ptr(), N, M, w_key.data_ptr(), w_value.data_ptr(), d,
+             dtype_code(mem), kv.data_ptr(), stream_of(dev))
     out = torch.empty_like(x)
     alpha = torch.empty(N, dtype=torch.float32, device=dev) if with_alpha else None
     stats = torch.empty((N, 4), dtype=torch.float32, device=dev) if with_stats else None
@@ -348,7 +375,8 @@ def gate_residual_rows(hidden: torch.Tensor, mem: torch.Tensor, w_kv: torch.Tens
 
 
 @gate_residual_rows.register_fake
-def _(hidden, mem, w_kv, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha, with_stats=False):
+def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha,
+      with_stats=False):
     n = hidden.numel() // hidden.shape[-1]
     res = [torch.empty_like(hidden)]
     if with_alpha:

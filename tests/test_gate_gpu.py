@@ -23,7 +23,9 @@ DEV = "cuda"
 def gate_path(request, monkeypatch):
     """Every test of this file runs on both gate paths of MicroEngram: the fused two-pass kernel
     (me_gate_residual) and, for few tokens, the library GEMM + row kernel (me_gate_rows)."""
-    monkeypatch.setattr(MicroEngram, "few_tokens_max", 0 if request.param == "fused" else 1 << 30)
+    limit = 0 if request.param == "fused" else 1 << 30
+    monkeypatch.setattr(MicroEngram, "few_tokens_max", limit)
+    monkeypatch.setattr(MicroEngram, "few_tokens_max_fp32", limit)
     return request.param
 
 
@@ -151,7 +153,7 @@ def test_grad_path_forward_equals_fused(dtype):
     # with gradients the forward hashes, gathers through the differentiable row lookup and
     # keeps the gate's row sums; its output is the fused inference forward's, bit for bit
     eng = _make(dtype, d=64, dim=8, heads=2, orders=(2, 3, 4)).train()
-    eng.few_tokens_max = 0  # the fused kernel, which the gradient path also runs
+    eng.few_tokens_max = eng.few_tokens_max_fp32 = 0  # the fused kernel, as the gradient path
     ids = torch.randint(0, 1000, (2, 70), device=DEV)
     hidden = torch.randn(2, 70, 64).to(dtype).to(DEV)
     with torch.no_grad():
@@ -244,8 +246,8 @@ def test_projection_rounds_to_nearest_even():
 @pytest.mark.parametrize("gate", [0, 1])
 @pytest.mark.parametrize("n,d,m", [(1, 64, 32), (37, 520, 96), (256, 1024, 256), (300, 5376, 1536)])
 def test_rows_path_matches_fused_and_oracle(hdt, tdt, gate, n, d, m):
-    # the few-token path (one GEMM against [W_K; W_V], then me_gate_rows) against the oracle and
-    # the fused kernel on the same operands, with a keep mask and the row stats of the backward
+    # the few-token path (me_kv_proj, then me_gate_rows) against the oracle and the fused kernel
+    # on the same operands, with a keep mask and the row stats of the backward
     g = torch.Generator().manual_seed(n * 7 + d)
     hidden = (torch.randn(n, d, generator=g) * 3).to(hdt)
     mem = (torch.randn(n, m, generator=g) * 0.5).to(tdt)
@@ -256,8 +258,7 @@ def test_rows_path_matches_fused_and_oracle(hdt, tdt, gate, n, d, m):
     keep = torch.rand(n, generator=g) > 0.2
     dev = [t.to(DEV) if t is not None else None for t in (hidden, mem, wk, wv, dq, dk, keep)]
     with torch.no_grad():
-        rows = ops.gate_residual_rows(dev[0], dev[1], torch.cat([dev[2], dev[3]]), dev[4], dev[5], gate,
-                                      dev[6], True, True)
+        rows = ops.gate_residual_rows(*dev[:6], gate, dev[6], True, True)
         fused = ops.gate_residual(*dev[:6], gate, dev[6], True, True)
     ref, alpha_ref = oracle.inject(hidden.float() if hdt == torch.float32 else hidden, mem, wk, wv,
                                    ["scalar", "scalar_sqrt"][gate], dq, dk, keep=keep, return_alpha=True)
@@ -269,6 +270,36 @@ def test_rows_path_matches_fused_and_oracle(hdt, tdt, gate, n, d, m):
     assert torch.allclose(rows[2][:, 0], fused[2][:, 0], rtol=1e-5)
     assert torch.equal(rows[2][:, 3], rows[1])
     assert torch.equal(rows[0][~dev[6]], dev[0][~dev[6]])  # keep = False: unchanged
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,d,m", [(1, 64, 32), (5, 24, 40), (128, 520, 96), (129, 256, 8),
+                                   (256, 5376, 1536), (300, 1024, 1024), (2048, 1024, 1024)])
+def test_kv_proj_matches_fp32_reference(dtype, n, d, m):
+    """me_kv_proj against torch's fp32 products of the same operands, rounded to the dtype:
+    [K | V] = round(mem W_K^T | mem W_V^T). Tolerance: the sums run in another order, so after
+    rounding an element may differ by one step of the dtype (bf16) or by 2e-6 of the sum of
+    |products| (fp32). Shapes cover one and several token tiles, model dims that are not a
+    multiple of 16 (the K / V boundary inside a 16-column block), mem dims that are not a
+    multiple of the k-step, and the serving decode shape. Where the sum cancels to near zero a
+    few fp32 roundings are many bf16 steps of the tiny result, hence the absolute term of 1e-6 of
+    the sum of |products| (a bound on fp32 accumulation error over these lengths)."""
+    g = torch.Generator().manual_seed(n + d + m)
+    mem = (torch.randn(n, m, generator=g) * 0.5).to(dtype)
+    wk = (torch.randn(d, m, generator=g) * 0.05).to(dtype)
+    wv = (torch.randn(d, m, generator=g) * 0.05).to(dtype)
+    got = ops.kv_proj(mem.to(DEV), wk.to(DEV), wv.to(DEV)).cpu()
+    exact = torch.cat([mem.double() @ wk.double().T, mem.double() @ wv.double().T], dim=1)
+    scale = torch.cat([mem.double().abs() @ wk.double().abs().T, mem.double().abs() @ wv.double().abs().T], 1)
+    assert got.shape == (n, 2 * d) and got.dtype == dtype
+    if dtype == torch.bfloat16:
+        want = exact.to(torch.bfloat16)
+        err = (got.double() - want.double()).abs()
+        bound = _bf16_ulp(torch.maximum(got.abs().float(), want.abs().float())).double() + 1e-6 * scale
+        assert bool((err <= bound).all()), float((err - bound).max())
+        assert float((got != want).float().mean()) < 0.02
+    else:
+        assert bool(((got.double() - exact).abs() <= 2e-6 * scale + 1e-30).all())
 
 
 def test_serving_decode_step_sampled():
