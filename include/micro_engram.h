@@ -281,6 +281,36 @@ int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const void *grad
              void *workspace, size_t workspace_size, void *stream);
 
 /*
+ * me_dedup_plan_size -- bytes of the segment plan me_dedup_keys writes for n keys.
+ */
+int me_dedup_plan_size(int64_t n, size_t *bytes);
+
+/*
+ * me_dedup_keys -- the key half of me_dedup: torch.unique(keys, return_inverse=True)
+ * (micro_engram/rows.py:81) plus a plan of which positions form each unique key's segment, so
+ * that me_dedup_sums can later add the gradient rows (rows.py:117-118) without sorting again.
+ * The keys depend only on the hashed row ids: a caller may run this half as soon as the forward
+ * has them, on another stream, and only the sums in the backward.
+ *
+ *   keys, n, key_bound, uniq, inv, count   as for me_dedup
+ *   plan       device buffer of at least me_dedup_plan_size(n) bytes, read by me_dedup_sums
+ *   workspace  at least me_dedup_workspace_size(n) bytes (free again when this call's work ends)
+ */
+int me_dedup_keys(const int64_t *keys, int64_t n, int64_t key_bound, int64_t *uniq, int64_t *inv,
+                  int64_t *count, void *plan, size_t plan_size, void *workspace,
+                  size_t workspace_size, void *stream);
+
+/*
+ * me_dedup_sums -- the gradient half of me_dedup: gsum row u = fp32 sum of the grads of the
+ * keys equal to uniq[u], added in increasing position from +0.0 (bit-exact with CPU index_add_,
+ * rows.py:117-118, 144-146), from the plan and count of an me_dedup_keys call on the same keys.
+ *
+ *   grads   [n, dim] of grad_dtype (ME_F32 / ME_BF16); gsum fp32 [n, dim] (rows past count unset)
+ */
+int me_dedup_sums(const void *plan, size_t plan_size, int64_t n, const int64_t *count,
+                  const void *grads, int grad_dtype, int32_t dim, float *gsum, void *stream);
+
+/*
  * me_sumsq -- sum of squares of n fp32 values into *out (or added to it when accumulate != 0),
  * in a fixed order. The squared gradient norm of RowTables.clip (micro_engram/rows.py:214-223).
  * workspace: at least 1 KiB.

@@ -11,16 +11,18 @@
 //   adam       micro_engram/optim.py:65-133, the sparse-gradient branch (88-97), per-row second
 //              moment (112-114) and write-back with stochastic_bf16 (33-44, 120-132)
 //
-// Dedup, two paths with the same results. Keys whose bits below a bucket fit 32 (the usual case:
-// table offset + row): a bucket pass on the high key bits, one LDS rank sort per bucket of
-// (low key bits, position) composites, and one workgroup per bucket that numbers its unique keys
-// after the earlier buckets', writes the unique keys and the inverse, and sums each segment's
-// gradient rows (bk_* kernels below). Wider keys: a stable LSD radix sort of (key, position)
-// pairs, 8 key bits per pass (per-block digit histograms, then a scatter that ranks equal
-// digits inside each wave with 8 ballots, lower lane = earlier element), segment heads, and
-// one thread per (segment, 4 columns) for the sums. Either way a segment's gradient rows are
-// summed in ascending position order starting from +0.0 -- the order, and so the rounding, of
-// CPU index_add_.
+// Dedup, in two halves: the keys (sorted unique keys, the inverse, and a segment plan: every
+// position in sorted key order, each unique key's first index and first position) depend
+// only on the row ids, and the sums read the gradients through the plan. Two key paths with the
+// same results. Keys whose bits below a group fit 32 (the usual case: table offset + row): three
+// launches -- per-tile grouping by the high key bits, one workgroup per group that sorts the
+// group's (low key bits, position) composites in LDS and counts its unique keys, and one that
+// numbers them after the earlier groups' and writes the unique keys, the inverse and the plan
+// (gd_* kernels below). Wider keys: a stable LSD radix sort of (key, position) pairs, 8 key bits
+// per pass (per-block digit histograms, then a scatter that ranks equal digits inside each wave
+// with 8 ballots, lower lane = earlier element), and segment heads. The sums: one thread per
+// (segment, 4 columns), a segment's gradient rows added in ascending position order starting
+// from +0.0 -- the order, and so the rounding, of CPU index_add_.
 #include "me_common.h"
 
 #include <algorithm>
@@ -144,6 +146,9 @@ __global__ __launch_bounds__(kThreads) void rs_scatter(const uint64_t *keys_in, 
 }
 
 // ---- segments of the sorted keys -------------------------------------------------------------
+// Both dedup paths leave a segment plan the sums read: spos (every position, in sorted key
+// order), seg_start (each unique key's first index into spos, then n) and seg_pos (each unique
+// key's first position, so the sums start its first row without going through spos).
 // Tile layout for the segment pass: thread t owns elements [t * kItems, (t + 1) * kItems) of
 // its block's tile, so a block-level exclusive scan of per-thread head counts numbers the heads.
 __device__ __forceinline__ bool is_head(const uint64_t *k, int64_t i) {
@@ -216,23 +221,25 @@ __global__ __launch_bounds__(kThreads) void seg_write(const uint64_t *skeys, con
     for (int i = 0; i < kItems; ++i) {
         const int64_t idx = b + i;
         if (idx >= n) break;
+        const uint32_t pos = spos[idx];
         if (is_head(skeys, idx)) {
             uniq[heads] = static_cast<int64_t>(skeys[idx]);
             seg_start[heads] = static_cast<uint32_t>(idx);
-            seg_pos[heads] = spos[idx];  // the segment's first row, one load less for the sums
+            seg_pos[heads] = pos;
             ++heads;
         }
-        inv[spos[idx]] = static_cast<int64_t>(heads) - 1;
+        inv[pos] = static_cast<int64_t>(heads) - 1;
         if (idx == n - 1) seg_start[heads] = static_cast<uint32_t>(n);
     }
 }
 
 __global__ void write_zero_count(int64_t *count) { *count = 0; }
 
-// One thread per (segment, run of kCols columns): the segment's gradient rows summed in sorted
-// (= original) order, starting from +0.0 like zeros().index_add_(). The segment's bounds, its
-// first row and the segment count are independent loads; rows after the first are fetched four
-// at a time and added in order.
+// ---- segment sums ----------------------------------------------------------------------------
+// Each unique key's gradient rows summed in sorted (= position) order, starting from +0.0 like
+// zeros().index_add_(). A thread owns one run of kCols columns of one segment: the segment's
+// bounds and first position are independent loads, and rows after the first are fetched
+// kSumBatch at a time (all positions, then all rows in flight) and added in order.
 __device__ __forceinline__ void load_cols(const float *p, float (&x)[4]) {
     const float4 v = *reinterpret_cast<const float4 *>(p);
     x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
@@ -249,11 +256,14 @@ __device__ __forceinline__ void load_cols(const uint16_t *p, float (&x)[1]) {
     x[0] = bf16_bits_to_float(*p);
 }
 
+// Rows of a segment past its first, loaded per step (positions, then rows, all in flight): the
+// longest segment (a hot key's repeats) is the kernel's critical path.
+constexpr int kSumBatch = 16;
+
 template <typename G, int kCols>
 __global__ __launch_bounds__(kThreads) void seg_sum(const G *grads, uint32_t dim, const uint32_t *spos,
                                                     const uint32_t *seg_start, const uint32_t *seg_pos,
-                                                    const int64_t *count, uint32_t max_segs,
-                                                    float *gsum) {
+                                                    const int64_t *count, uint32_t max_segs, float *gsum) {
     const uint32_t runs = dim / kCols;
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     const uint32_t seg = t / runs;
@@ -265,23 +275,19 @@ __global__ __launch_bounds__(kThreads) void seg_sum(const G *grads, uint32_t dim
     load_cols(grads + static_cast<uint64_t>(first) * dim + c0, x);
 #pragma unroll
     for (int c = 0; c < kCols; ++c) acc[c] = 0.f + x[c];
-    uint32_t i = lo + 1;
-    for (; i + 4 <= hi; i += 4) {
-        uint32_t q[4];
-        float y[4][kCols];
+    for (uint32_t i = lo + 1; i < hi; i += kSumBatch) {
+        const uint32_t m = hi - i < static_cast<uint32_t>(kSumBatch) ? hi - i : kSumBatch;
+        uint32_t q[kSumBatch];
+        float y[kSumBatch][kCols];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) q[u] = spos[i + u];
+        for (int v = 0; v < kSumBatch; ++v) q[v] = static_cast<uint32_t>(v) < m ? spos[i + v] : first;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) load_cols(grads + static_cast<uint64_t>(q[u]) * dim + c0, y[u]);
+        for (int v = 0; v < kSumBatch; ++v) load_cols(grads + static_cast<uint64_t>(q[v]) * dim + c0, y[v]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int v = 0; v < kSumBatch; ++v)
+            if (static_cast<uint32_t>(v) < m)
 #pragma unroll
-            for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + y[u][c];
-    }
-    for (; i < hi; ++i) {
-        load_cols(grads + static_cast<uint64_t>(spos[i]) * dim + c0, x);
-#pragma unroll
-        for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + x[c];
+                for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + y[v][c];
     }
     float *out = gsum + static_cast<uint64_t>(seg) * dim + c0;
     if constexpr (kCols == 4)
@@ -290,136 +296,105 @@ __global__ __launch_bounds__(kThreads) void seg_sum(const G *grads, uint32_t dim
         out[0] = acc[0];
 }
 
-// ---- bucket dedup -----------------------------------------------------------------------------
-// The dedup when keys fit 32 bits below a bucket: every (key, position) goes to the bucket of
-// its high key bits (key >> shift, ~24 keys per bucket on average), one workgroup per bucket
-// sorts the bucket's (low key bits, position) composites -- distinct because positions are, so
-// their order is the stable order of the keys -- and counts its unique keys, and one workgroup
-// per bucket writes the unique keys, the inverse and the segments (in the layout seg_sum reads)
-// numbered after the earlier buckets' unique keys. Five launches in place of two per 8-bit
-// digit of a radix sort, and no device-scope atomics on hot counters (they cost tens of
-// microseconds here): per-tile histograms in LDS, a [tile][bucket] matrix of counts and a
-// prefix over it, and the scatter's slots from LDS counters seeded with each tile's bases.
-// Buckets larger than LDS (many repeats of few keys) are sorted in global memory by their
-// workgroup with a stable LSD radix sort.
-constexpr int kBucketCap = kTile;        // composites a bucket may sort in LDS (2048)
-constexpr int kBkTile = kTile;           // keys per workgroup of the histogram and the scatter
-constexpr uint32_t kBkMaxBuckets = 8192; // LDS counters per workgroup
+// ---- group dedup ------------------------------------------------------------------------------
+// The dedup when the key bits below a group fit 32: a key's group is its high bits (key >>
+// shift, a few hundred keys per group on average), and the composites (low key bits << 32 |
+// position) of one group are distinct, so their order is the stable order of the keys. Three
+// launches, no device-scope atomics:
+//   gd_tile   per tile of 2048 keys: an LDS histogram over the groups, its exclusive prefix
+//             (the tile's offset of every group, written as a row of `off`), and the tile's
+//             composites grouped by group into its slice of tile_comp;
+//   gd_group  per group: its runs from every tile gathered into LDS, bucketed by the top 8 low
+//             key bits, each composite ranked inside its bucket (the rest of a bucket is a few
+//             composites, or the repeats of one hot key), written sorted into comp at the
+//             group's start (the sum of its offsets over the tiles), its unique keys counted;
+//   gd_emit   per group: its unique keys numbered after the earlier groups' (a block sum of
+//             their counts), then uniq, inv and the segment plan.
+// A group larger than LDS is sorted by its workgroup in global memory (stable LSD radix sort).
+constexpr int kGdTile = kTile;            // keys per gd_tile workgroup
+constexpr uint32_t kGdMaxGroups = 1024;   // groups (LDS counters of gd_tile)
+constexpr uint32_t kGdMaxTiles = 1024;    // tiles (n up to 2^21)
+constexpr int kGdCap = 2048;              // composites a group may sort in LDS
+constexpr int64_t kGdMean = 256;          // keys per group aimed at (at most twice that)
+constexpr int kGdSubBits = 10;            // a group's LDS sort: buckets of its top low key bits
+constexpr int kGdSub = 1 << kGdSubBits;
 
-// Bucket of a key; keys outside [0, key_bound) (outside the contract) land in the last bucket
+// Group of a key; keys outside [0, key_bound) (outside the contract) land in the last group
 // instead of outside the arrays.
-__device__ __forceinline__ uint32_t bucket_of(uint64_t key, int shift, uint32_t nb) {
-    const uint64_t b = key >> shift;
-    return b < nb ? static_cast<uint32_t>(b) : nb - 1;
+__device__ __forceinline__ uint32_t group_of(uint64_t key, int shift, uint32_t ng) {
+    const uint64_t g = key >> shift;
+    return g < ng ? static_cast<uint32_t>(g) : ng - 1;
 }
 
-__device__ __forceinline__ uint64_t composite(uint64_t key, uint64_t base, uint32_t pos) {
-    return ((key - base) << 32) | pos;
+__device__ __forceinline__ uint64_t composite(uint64_t key, uint32_t g, int shift, uint32_t pos) {
+    return ((key - (static_cast<uint64_t>(g) << shift)) << 32) | pos;
 }
 
-// Tile t's bucket counts into mat[t * nb + b] (coalesced rows).
-__global__ __launch_bounds__(kThreads) void bk_hist(const uint64_t *keys, int64_t n, int shift,
-                                                    uint32_t nb, uint32_t *mat) {
-    __shared__ uint32_t s_h[kBkMaxBuckets];
-    const int tid = threadIdx.x;
-    for (uint32_t b = tid; b < nb; b += kThreads) s_h[b] = 0u;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBkTile;
-    uint64_t k[kItems];
-#pragma unroll
-    for (int e = 0; e < kItems; ++e) {
-        const int64_t i = base + e * kThreads + tid;
-        k[e] = i < n ? keys[i] : ~0ull;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < kItems; ++e)
-        if (base + e * kThreads + tid < n) atomicAdd(&s_h[bucket_of(k[e], shift, nb)], 1u);
-    __syncthreads();
-    uint32_t *row = mat + static_cast<uint64_t>(blockIdx.x) * nb;
-    for (uint32_t b = tid; b < nb; b += kThreads) row[b] = s_h[b];
-}
-
-// One thread per bucket: its column of tile counts becomes the exclusive prefix over the tiles
-// (in place), its total is scanned within the block (excl[b]) and the block's sum goes to btot.
-__global__ __launch_bounds__(kThreads) void bk_prefix(uint32_t *mat, uint32_t nb, uint32_t ntiles,
-                                                      uint32_t *excl, uint32_t *btot) {
-    __shared__ uint32_t s_wtot[kThreads / 64];
+// Exclusive scan of the 256 per-thread values v across the workgroup; *total gets the sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s_wtot, uint32_t *total) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t b = blockIdx.x * kThreads + tid;
-    uint32_t tot = 0;
-    if (b < nb) {
-        uint32_t t = 0;
-        for (; t + 32 <= ntiles; t += 32) {
-            uint32_t c[32];
-#pragma unroll
-            for (int u = 0; u < 32; ++u) c[u] = mat[static_cast<uint64_t>(t + u) * nb + b];
-#pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                mat[static_cast<uint64_t>(t + u) * nb + b] = tot;
-                tot += c[u];
-            }
-        }
-        for (; t < ntiles; ++t) {
-            const uint32_t c = mat[static_cast<uint64_t>(t) * nb + b];
-            mat[static_cast<uint64_t>(t) * nb + b] = tot;
-            tot += c;
-        }
-    }
-    const uint32_t incl = wave_inclusive_scan(tot, lane);
+    const uint32_t incl = wave_inclusive_scan(v, lane);
     if (lane == 63) s_wtot[wave] = incl;
     __syncthreads();
     uint32_t before = 0, all = 0;
+#pragma unroll
     for (int w = 0; w < kThreads / 64; ++w) {
-        if (w < wave) before += s_wtot[w];
-        all += s_wtot[w];
+        const uint32_t x = s_wtot[w];
+        before += w < wave ? x : 0u;
+        all += x;
     }
-    if (b < nb) excl[b] = before + incl - tot;
-    if (tid == 0) btot[blockIdx.x] = all;
+    __syncthreads();  // s_wtot may be reused
+    *total = all;
+    return before + incl - v;
 }
 
-// Exclusive prefix of the (<= 32) block sums of bk_prefix, into s_bp, by wave 0.
-__device__ __forceinline__ void block_prefix(const uint32_t *btot, uint32_t nb, uint32_t *s_bp, int tid) {
-    const uint32_t nblk = (nb + kThreads - 1) / kThreads;
-    if (tid < 64) {
-        const uint32_t v = static_cast<uint32_t>(tid) < nblk ? btot[tid] : 0u;
-        const uint32_t incl = wave_inclusive_scan(v, tid);
-        if (static_cast<uint32_t>(tid) < nblk) s_bp[tid] = incl - v;
-    }
-}
-
-// Each tile's keys into their buckets: slot = bucket start + the bucket's keys in earlier tiles
-// + an LDS counter (the order inside a bucket is arbitrary: bk_sort orders by position). The
-// blocks also write the bucket starts (start[nb] = n).
-__global__ __launch_bounds__(kThreads) void bk_scatter(const uint64_t *keys, int64_t n, int shift,
-                                                       uint32_t nb, const uint32_t *mat,
-                                                       const uint32_t *excl, const uint32_t *btot,
-                                                       uint64_t *bkeys, uint32_t *bpos,
-                                                       uint32_t *start) {
-    __shared__ uint32_t s_base[kBkMaxBuckets];
-    __shared__ uint32_t s_bp[kBkMaxBuckets / kThreads];
+// Tile t: counts per group, their exclusive prefix as row t of off ([tiles][ng + 1]), and the
+// tile's composites at tile_comp[t * kGdTile + prefix + slot] (slots by LDS counters).
+__global__ __launch_bounds__(kThreads) void gd_tile(const uint64_t *keys, int64_t n, int shift, uint32_t ng,
+                                                    uint64_t *tile_comp, uint32_t *off) {
+    __shared__ uint32_t s_cnt[kGdMaxGroups + 1];
+    __shared__ uint32_t s_wtot[kThreads / 64];
     const int tid = threadIdx.x;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBkTile;
+    for (uint32_t g = tid; g <= ng; g += kThreads) s_cnt[g] = 0u;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kGdTile;
     uint64_t k[kItems];
 #pragma unroll
     for (int e = 0; e < kItems; ++e) {
         const int64_t i = base + e * kThreads + tid;
         k[e] = i < n ? keys[i] : 0ull;
     }
-    block_prefix(btot, nb, s_bp, tid);
     __syncthreads();
-    const uint32_t *row = mat + static_cast<uint64_t>(blockIdx.x) * nb;
-    for (uint32_t b = tid; b < nb; b += kThreads) s_base[b] = s_bp[b / kThreads] + excl[b] + row[b];
-    for (uint32_t b = blockIdx.x * kThreads + tid; b < nb; b += gridDim.x * kThreads)
-        start[b] = s_bp[b / kThreads] + excl[b];
-    if (blockIdx.x == 0 && tid == 0) start[nb] = static_cast<uint32_t>(n);
+#pragma unroll
+    for (int e = 0; e < kItems; ++e)
+        if (base + e * kThreads + tid < n) atomicAdd(&s_cnt[group_of(k[e], shift, ng)], 1u);
     __syncthreads();
+    // exclusive prefix over the groups: thread tid owns groups [tid * per, tid * per + per)
+    const uint32_t per = (ng + kThreads - 1) / kThreads;
+    const uint32_t g0 = static_cast<uint32_t>(tid) * per;
+    uint32_t mine = 0;
+    for (uint32_t q = 0; q < per; ++q)
+        if (g0 + q < ng) mine += s_cnt[g0 + q];
+    uint32_t total;
+    uint32_t run = block_exclusive_scan(mine, s_wtot, &total);
+    for (uint32_t q = 0; q < per; ++q)
+        if (g0 + q < ng) {
+            const uint32_t c = s_cnt[g0 + q];
+            s_cnt[g0 + q] = run;
+            run += c;
+        }
+    if (tid == 0) s_cnt[ng] = total;
+    __syncthreads();
+    uint32_t *row = off + static_cast<uint64_t>(blockIdx.x) * (ng + 1);
+    for (uint32_t g = tid; g <= ng; g += kThreads) row[g] = s_cnt[g];
+    __syncthreads();  // the row is read before the counters move on
+    uint64_t *out = tile_comp + base;
 #pragma unroll
     for (int e = 0; e < kItems; ++e) {
         const int64_t i = base + e * kThreads + tid;
         if (i < n) {
-            const uint32_t slot = atomicAdd(&s_base[bucket_of(k[e], shift, nb)], 1u);
-            bkeys[slot] = k[e];
-            bpos[slot] = static_cast<uint32_t>(i);
+            const uint32_t g = group_of(k[e], shift, ng);
+            const uint32_t slot = atomicAdd(&s_cnt[g], 1u);
+            out[slot] = composite(k[e], g, shift, static_cast<uint32_t>(i));
         }
     }
 }
@@ -468,9 +443,9 @@ __device__ void wg_radix_sort(uint64_t *a, uint64_t *t, uint32_t n, int bits) {
             if (valid && rank == 0) s_wcnt[wave][digit] = static_cast<uint32_t>(__popcll(same));
             __syncthreads();
             if (valid) {
-                uint32_t off = s_hist[digit] + static_cast<uint32_t>(rank);
-                for (int w = 0; w < wave; ++w) off += s_wcnt[w][digit];
-                dst[off] = v;
+                uint32_t o = s_hist[digit] + static_cast<uint32_t>(rank);
+                for (int w = 0; w < wave; ++w) o += s_wcnt[w][digit];
+                dst[o] = v;
             }
             __syncthreads();
             uint32_t add = 0;
@@ -488,235 +463,232 @@ __device__ void wg_radix_sort(uint64_t *a, uint64_t *t, uint32_t n, int bits) {
     __syncthreads();
 }
 
-// Rank sort of the n (<= ITEMS * 256) distinct composites in s_c into out: each composite's
-// rank is how many are smaller (every lane reads the same s_c[j] at once, an LDS broadcast);
-// returns how many of this thread's composites are the first of their key.
-template <int ITEMS>
-__device__ __forceinline__ uint32_t rank_sort(const uint64_t *s_c, uint32_t n, uint64_t *out, int tid) {
-    uint64_t mine[ITEMS];
-    uint32_t rank[ITEMS], same_before[ITEMS];
-#pragma unroll
-    for (int e = 0; e < ITEMS; ++e) {
-        const uint32_t i = tid + e * kThreads;
-        mine[e] = i < n ? s_c[i] : ~0ull;
-        rank[e] = 0u;
-        same_before[e] = 0u;
-    }
-    uint32_t j = 0;
-    for (; j + 4 <= n; j += 4) {
-        uint64_t c[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) c[u] = s_c[j + u];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int e = 0; e < ITEMS; ++e) {
-                const bool less = c[u] < mine[e];
-                rank[e] += less ? 1u : 0u;
-                same_before[e] += (less && (c[u] >> 32) == (mine[e] >> 32)) ? 1u : 0u;
-            }
-    }
-    for (; j < n; ++j) {
-        const uint64_t c = s_c[j];
-#pragma unroll
-        for (int e = 0; e < ITEMS; ++e) {
-            const bool less = c < mine[e];
-            rank[e] += less ? 1u : 0u;
-            same_before[e] += (less && (c >> 32) == (mine[e] >> 32)) ? 1u : 0u;
-        }
-    }
-    uint32_t heads = 0;
-#pragma unroll
-    for (int e = 0; e < ITEMS; ++e)
-        if (tid + e * kThreads < n) {
-            out[rank[e]] = mine[e];
-            heads += same_before[e] == 0u ? 1u : 0u;  // the first of its key
-        }
-    return heads;
-}
-
-// One workgroup per bucket: the bucket's composites sorted into comp[lo, hi) -- a rank sort in
-// LDS (each composite's rank = how many are smaller; every lane reads the same s_c[j] at once,
-// an LDS broadcast), or the global radix sort above for buckets larger than LDS -- and the
-// number of unique keys in it into ucount[b].
-__global__ __launch_bounds__(kThreads) void bk_sort(const uint64_t *bkeys, const uint32_t *bpos,
-                                                    const uint32_t *start, int shift, uint64_t *comp,
-                                                    uint64_t *tmp, uint32_t *ucount) {
-    __shared__ uint64_t s_c[kBucketCap];
+// Group g: its composites sorted into comp[gstart[g], gstart[g] + size) and its unique key
+// count into ucount[g]. The runs: tile t holds the group's composites at off[t][g] ..
+// off[t][g + 1] of its slice; the group starts at the sum of off[t][g] over the tiles (every
+// key of an earlier group, in every tile).
+__global__ __launch_bounds__(kThreads) void gd_group(const uint64_t *tile_comp, const uint32_t *off,
+                                                     uint32_t ntiles, uint32_t ng, int shift, int64_t n,
+                                                     uint64_t *comp, uint64_t *tmp, uint32_t *gstart,
+                                                     uint32_t *ucount) {
+    __shared__ uint64_t s_a[kGdCap];
+    __shared__ uint64_t s_b[kGdCap];
+    __shared__ uint16_t s_map[kGdCap];           // run (tile) of each of the group's composites
+    __shared__ uint32_t s_run[kGdMaxTiles + 1];  // run t lands at [s_run[t], s_run[t + 1])
+    __shared__ uint32_t s_src[kGdMaxTiles];      // run t's first index into tile_comp
+    __shared__ uint32_t s_sb[kGdSub + 1];        // bucket starts
+    __shared__ uint32_t s_cur[kGdSub];           // bucket fill counters
+    __shared__ uint32_t s_wtot[kThreads / 64];
     __shared__ uint32_t s_red[kThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t b = blockIdx.x;
-    const uint32_t lo = start[b], n = start[b + 1] - lo;
-    const uint64_t base = static_cast<uint64_t>(b) << shift;
+    const uint32_t g = blockIdx.x;
+    // ---- the runs: thread tid owns tiles [tid * per, tid * per + per)
+    const uint32_t per = (ntiles + kThreads - 1) / kThreads;
+    const uint32_t t0 = static_cast<uint32_t>(tid) * per;
+    uint32_t lo[4], len[4];  // per <= 4 (ntiles <= 1024)
+    uint32_t mine = 0, before_sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        lo[q] = 0u;
+        len[q] = 0u;
+        if (static_cast<uint32_t>(q) < per && t0 + q < ntiles) {
+            const uint32_t *row = off + static_cast<uint64_t>(t0 + q) * (ng + 1);
+            lo[q] = row[g];
+            len[q] = row[g + 1] - lo[q];
+            mine += len[q];
+            before_sum += lo[q];
+        }
+    }
+    uint32_t size, gs;
+    uint32_t run = block_exclusive_scan(mine, s_wtot, &size);
+    block_exclusive_scan(before_sum, s_wtot, &gs);
+    const bool in_lds = size <= static_cast<uint32_t>(kGdCap);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (static_cast<uint32_t>(q) < per && t0 + q < ntiles) {
+            s_run[t0 + q] = run;
+            s_src[t0 + q] = (t0 + q) * static_cast<uint32_t>(kGdTile) + lo[q];
+            if (in_lds)
+                for (uint32_t j = 0; j < len[q]; ++j) s_map[run + j] = static_cast<uint16_t>(t0 + q);
+            run += len[q];
+        }
+    if (tid == 0) {
+        s_run[ntiles] = size;
+        gstart[g] = gs;
+        if (g == ng - 1) gstart[ng] = static_cast<uint32_t>(n);
+    }
+    __syncthreads();
+    // composite k of the group: k - s_run[t] into run t
+    auto src_of = [&](uint32_t k, uint32_t t) { return s_src[t] + (k - s_run[t]); };
     uint32_t heads = 0;
-    if (n <= static_cast<uint32_t>(kBucketCap)) {
-        for (uint32_t i = tid; i < n; i += kThreads) s_c[i] = composite(bkeys[lo + i], base, bpos[lo + i]);
+    if (in_lds) {
+        {   // every source index first, then all loads in flight at once
+            constexpr int kPer = kGdCap / kThreads;
+            uint32_t src[kPer];
+            uint64_t v[kPer];
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const uint32_t k = tid + j * kThreads;
+                src[j] = k < size ? src_of(k, s_map[k]) : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < kPer; ++j)
+                if (tid + j * kThreads < size) v[j] = tile_comp[src[j]];
+#pragma unroll
+            for (int j = 0; j < kPer; ++j)
+                if (tid + j * kThreads < size) s_a[tid + j * kThreads] = v[j];
+        }
+        // buckets of the top sbits low key bits
+        const int sbits = shift < kGdSubBits ? shift : kGdSubBits;
+        const uint32_t nsub = 1u << sbits;
+        const int sh = 32 + shift - sbits;
+        auto sub = [&](uint64_t c) { return static_cast<uint32_t>(c >> sh) & (nsub - 1); };
+        constexpr int kSubPer = kGdSub / kThreads;
+#pragma unroll
+        for (int q = 0; q < kSubPer; ++q) s_cur[tid * kSubPer + q] = 0u;
         __syncthreads();
-        // as many items per thread as the bucket needs (a uniform branch)
-        if (n <= kThreads)
-            heads = rank_sort<1>(s_c, n, comp + lo, tid);
-        else if (n <= 2 * kThreads)
-            heads = rank_sort<2>(s_c, n, comp + lo, tid);
-        else if (n <= 4 * kThreads)
-            heads = rank_sort<4>(s_c, n, comp + lo, tid);
-        else
-            heads = rank_sort<kItems>(s_c, n, comp + lo, tid);
+        for (uint32_t k = tid; k < size; k += kThreads) atomicAdd(&s_cur[sub(s_a[k])], 1u);
+        __syncthreads();
+        {   // bucket starts: thread tid owns buckets [tid * kSubPer, tid * kSubPer + kSubPer)
+            uint32_t c[kSubPer], sum = 0;
+#pragma unroll
+            for (int q = 0; q < kSubPer; ++q) {
+                c[q] = s_cur[tid * kSubPer + q];
+                sum += c[q];
+            }
+            uint32_t tot;
+            uint32_t st = block_exclusive_scan(sum, s_wtot, &tot);
+#pragma unroll
+            for (int q = 0; q < kSubPer; ++q) {
+                s_sb[tid * kSubPer + q] = st;
+                s_cur[tid * kSubPer + q] = st;
+                st += c[q];
+            }
+            if (tid == 0) s_sb[kGdSub] = size;
+        }
+        __syncthreads();
+        for (uint32_t k = tid; k < size; k += kThreads) {
+            const uint64_t c = s_a[k];
+            s_b[atomicAdd(&s_cur[sub(c)], 1u)] = c;
+        }
+        __syncthreads();
+        // rank inside the bucket (buckets past nsub are empty and start at size), four LDS
+        // reads in flight per step, the last step masked; keys and positions compared as 32-bit
+        // halves (a composite is less when its key is, or its key is equal and its position is)
+        for (uint32_t k = tid; k < size; k += kThreads) {
+            const uint64_t c = s_b[k];
+            const uint32_t ck = static_cast<uint32_t>(c >> 32), cp = static_cast<uint32_t>(c);
+            const uint32_t j = sub(c);
+            const uint32_t blo = s_sb[j], bhi = s_sb[j + 1];
+            uint32_t rank = 0, same = 0;
+            for (uint32_t m = blo; m < bhi; m += 4) {
+                uint64_t d[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) d[q] = s_b[m + q < bhi ? m + q : k];  // k: never less
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t dk = static_cast<uint32_t>(d[q] >> 32), dp = static_cast<uint32_t>(d[q]);
+                    rank += dk < ck ? 1u : 0u;
+                    same += (dk == ck && dp < cp) ? 1u : 0u;
+                }
+            }
+            rank += same;
+            s_a[blo + rank] = c;  // s_a is free again: every composite is in s_b
+            heads += same == 0u ? 1u : 0u;
+        }
+        __syncthreads();
+        for (uint32_t k = tid; k < size; k += kThreads) comp[gs + k] = s_a[k];
     } else {
-        uint64_t *a = comp + lo;
-        for (uint32_t i = tid; i < n; i += kThreads) a[i] = composite(bkeys[lo + i], base, bpos[lo + i]);
+        uint64_t *a = comp + gs;
+        for (uint32_t k = tid; k < size; k += kThreads) {
+            uint32_t lo_t = 0, hi_t = ntiles;  // s_run[lo_t] <= k < s_run[hi_t]
+            while (hi_t - lo_t > 1) {
+                const uint32_t m = (lo_t + hi_t) >> 1;
+                if (s_run[m] <= k) lo_t = m; else hi_t = m;
+            }
+            a[k] = tile_comp[src_of(k, lo_t)];
+        }
         __syncthreads();
-        wg_radix_sort(a, tmp + lo, n, 32 + shift);
-        for (uint32_t i = tid; i < n; i += kThreads) heads += (i == 0 || (a[i] >> 32) != (a[i - 1] >> 32)) ? 1u : 0u;
+        wg_radix_sort(a, tmp + gs, size, 32 + shift);
+        for (uint32_t i = tid; i < size; i += kThreads)
+            heads += (i == 0 || (a[i] >> 32) != (a[i - 1] >> 32)) ? 1u : 0u;
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) heads += __shfl_xor(heads, off, 64);
+    for (int o = 32; o >= 1; o >>= 1) heads += __shfl_xor(heads, o, 64);
     if (lane == 0) s_red[wave] = heads;
     __syncthreads();
-    if (tid == 0) {
-        uint32_t t = 0;
-        for (int w = 0; w < kThreads / 64; ++w) t += s_red[w];
-        ucount[b] = t;
-    }
+    if (tid == 0) ucount[g] = s_red[0] + s_red[1] + s_red[2] + s_red[3];
 }
 
-// The fp32 sum of rows pos(a), pos(a+1), ... pos(e-1), columns [c0, c0 + kCols), added in that
-// order from +0.0 (the rounding of CPU index_add_), into out.
-template <typename G, int kCols, typename PosAt>
-__device__ __forceinline__ void sum_segment(const G *grads, uint32_t dim, uint32_t c0, uint32_t a,
-                                            uint32_t e, PosAt pos_at, float *out) {
-    float acc[kCols], x[kCols];
-    load_cols(grads + static_cast<uint64_t>(pos_at(a)) * dim + c0, x);
-#pragma unroll
-    for (int c = 0; c < kCols; ++c) acc[c] = 0.f + x[c];
-    uint32_t i = a + 1;
-    for (; i + 4 <= e; i += 4) {
-        float y[4][kCols];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) load_cols(grads + static_cast<uint64_t>(pos_at(i + u)) * dim + c0, y[u]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + y[u][c];
-    }
-    for (; i < e; ++i) {
-        load_cols(grads + static_cast<uint64_t>(pos_at(i)) * dim + c0, x);
-#pragma unroll
-        for (int c = 0; c < kCols; ++c) acc[c] = acc[c] + x[c];
-    }
-    if constexpr (kCols == 4)
-        *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    else
-        out[0] = acc[0];
-}
-
-// One workgroup per bucket: its unique keys are numbered after those of the buckets before it
-// (a block sum over ucount[0, b)); it writes uniq, inv and, with gradients, each unique key's
-// fp32 sum of its gradient rows in increasing position order (bit-exact with CPU index_add_).
-// The bucket's positions and segment starts are staged in LDS, and the workgroup sums every
-// (segment, run of kCols columns) with all its threads; a bucket larger than LDS (rare: many
-// repeats of few keys) has each segment summed by the thread of its first element. The last
-// bucket writes the count.
-template <typename G, int kCols>
-__global__ __launch_bounds__(kThreads) void bk_emit(const uint64_t *comp, const uint32_t *start,
-                                                    const uint32_t *ucount, uint32_t nb, int shift,
-                                                    const G *grads, uint32_t dim, int64_t *uniq,
-                                                    int64_t *inv, float *gsum, int64_t *count) {
-    __shared__ uint32_t s_scan[kThreads];
-    __shared__ uint32_t s_red[kThreads / 64];
-    __shared__ uint32_t s_pos[kBucketCap];
-    __shared__ uint32_t s_seg[kBucketCap + 1];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t b = blockIdx.x;
-    const uint32_t lo = start[b], n = start[b + 1] - lo;
-    const uint64_t base = static_cast<uint64_t>(b) << shift;
+// Group g: its unique keys numbered after the earlier groups' (a block sum over ucount[0, g));
+// writes uniq, inv and the plan (spos, seg_start, seg_pos). The last group writes the count and the end
+// of the last segment.
+__global__ __launch_bounds__(kThreads) void gd_emit(const uint64_t *comp, const uint32_t *gstart,
+                                                    const uint32_t *ucount, uint32_t ng, int shift,
+                                                    int64_t *uniq, int64_t *inv, uint32_t *spos,
+                                                    uint32_t *seg_start, uint32_t *seg_pos,
+                                                    int64_t *count) {
+    __shared__ uint64_t s_c[kGdCap];
+    __shared__ uint32_t s_wtot[kThreads / 64];
+    const int tid = threadIdx.x;
+    const uint32_t g = blockIdx.x;
+    const uint32_t lo = gstart[g], size = gstart[g + 1] - lo;
+    const uint64_t gbase = static_cast<uint64_t>(g) << shift;
     const uint64_t *sorted = comp + lo;
-    const bool in_lds = n <= static_cast<uint32_t>(kBucketCap);
-    // unique keys of the earlier buckets: 16-byte loads, all of a thread's issued together
-    uint32_t before = 0;
-    {
-        const uint4 *u4 = reinterpret_cast<const uint4 *>(ucount);
-        const uint32_t words = (b + 3) / 4;  // ucount is padded to a multiple of 4 entries
-        for (uint32_t w0 = tid; w0 < words; w0 += 4 * kThreads) {
-            uint4 x[4];
+    const bool in_lds = size <= static_cast<uint32_t>(kGdCap);
+    if (in_lds) {  // the group's composites into LDS, every load in flight at once
+        constexpr int kPer = kGdCap / kThreads;
+        uint64_t v[kPer];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t w = w0 + q * kThreads;
-                x[q] = w < words ? u4[w] : make_uint4(0u, 0u, 0u, 0u);
-            }
+        for (int j = 0; j < kPer; ++j)
+            if (tid + j * kThreads < size) v[j] = sorted[tid + j * kThreads];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t j = 4 * (w0 + q * kThreads);
-                before += (j + 0 < b ? x[q].x : 0u) + (j + 1 < b ? x[q].y : 0u) +
-                          (j + 2 < b ? x[q].z : 0u) + (j + 3 < b ? x[q].w : 0u);
-            }
-        }
+        for (int j = 0; j < kPer; ++j)
+            if (tid + j * kThreads < size) s_c[tid + j * kThreads] = v[j];
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) before += __shfl_xor(before, off, 64);
-    if (lane == 0) s_red[wave] = before;
-    __syncthreads();
-    uint32_t run = 0;  // unique keys numbered before this tile
-    for (int w = 0; w < kThreads / 64; ++w) run += s_red[w];
-    const uint32_t first_u = run;
-    if (b == nb - 1 && tid == 0) *count = static_cast<int64_t>(run) + ucount[b];
-    const uint32_t runs = dim / kCols;
-    for (uint32_t t0 = 0; t0 < n; t0 += kThreads * kItems) {
-        const uint32_t i0 = t0 + static_cast<uint32_t>(tid) * kItems;
+    uint32_t prior = 0;
+    for (uint32_t q = tid; q < g; q += kThreads) prior += ucount[q];
+    uint32_t run;
+    block_exclusive_scan(prior, s_wtot, &run);  // run = unique keys of the earlier groups (the
+                                                // scan's barriers also publish s_c)
+    if (g == ng - 1 && tid == 0) {
+        const uint32_t total = run + ucount[g];
+        *count = static_cast<int64_t>(total);
+        seg_start[total] = lo + size;
+    }
+    auto item = [&](uint32_t i) { return in_lds ? s_c[i] : sorted[i]; };
+    for (uint32_t c0 = 0; c0 < size; c0 += kThreads * kItems) {
+        const uint32_t i0 = c0 + static_cast<uint32_t>(tid) * kItems;
         uint64_t v[kItems];
-        uint32_t c = 0;
-#pragma unroll
-        for (int e = 0; e < kItems; ++e) v[e] = i0 + e < n ? sorted[i0 + e] : 0ull;
-        const uint64_t prev = i0 > 0 && i0 < n ? sorted[i0 - 1] : ~0ull;
         bool head[kItems];
-#pragma unroll
-        for (int e = 0; e < kItems; ++e) {
-            const uint64_t p = e == 0 ? prev : v[e - 1];
-            head[e] = i0 + e < n && (i0 + e == 0 || (v[e] >> 32) != (p >> 32));
-            c += head[e] ? 1u : 0u;
-        }
-        s_scan[tid] = c;
-        __syncthreads();
-        for (int off = 1; off < kThreads; off <<= 1) {
-            const uint32_t x = tid >= off ? s_scan[tid - off] : 0u;
-            __syncthreads();
-            s_scan[tid] += x;
-            __syncthreads();
-        }
-        uint32_t u = run + s_scan[tid] - c;  // unique keys before this thread's first element
+        uint32_t nh = 0;
+        uint64_t prev = i0 > 0 && i0 < size ? item(i0 - 1) : ~0ull;
 #pragma unroll
         for (int e = 0; e < kItems; ++e) {
             const uint32_t i = i0 + e;
-            if (i < n) {
+            v[e] = i < size ? item(i) : ~0ull;
+            head[e] = i < size && (i == 0 || (v[e] >> 32) != (prev >> 32));
+            nh += head[e] ? 1u : 0u;
+            prev = v[e];
+        }
+        uint32_t chunk_heads;
+        uint32_t u = run + block_exclusive_scan(nh, s_wtot, &chunk_heads);
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) {
+            const uint32_t i = i0 + e;
+            if (i < size) {
                 const uint32_t pos = static_cast<uint32_t>(v[e]);
                 if (head[e]) {
-                    uniq[u] = static_cast<int64_t>(base + (v[e] >> 32));
-                    if (in_lds) {
-                        s_seg[u - first_u] = i;
-                    } else if (grads != nullptr) {
-                        uint32_t end = i + 1;
-                        while (end < n && (sorted[end] >> 32) == (v[e] >> 32)) ++end;
-                        for (uint32_t r = 0; r < runs; ++r)
-                            sum_segment<G, kCols>(grads, dim, r * kCols, i, end,
-                                                  [&](uint32_t k) { return static_cast<uint32_t>(sorted[k]); },
-                                                  gsum + static_cast<uint64_t>(u) * dim + r * kCols);
-                    }
+                    uniq[u] = static_cast<int64_t>(gbase + (v[e] >> 32));
+                    seg_start[u] = lo + i;
+                    seg_pos[u] = pos;
                     ++u;
                 }
                 inv[pos] = static_cast<int64_t>(u) - 1;
-                if (in_lds) s_pos[i] = pos;
+                spos[lo + i] = pos;
             }
         }
-        run += s_scan[kThreads - 1];
-        __syncthreads();
-    }
-    if (grads == nullptr || !in_lds) return;
-    const uint32_t nseg = run - first_u;
-    if (tid == 0) s_seg[nseg] = n;
-    __syncthreads();
-    for (uint32_t it = tid; it < nseg * runs; it += kThreads) {
-        const uint32_t j = it / runs, c0 = (it - j * runs) * kCols;
-        sum_segment<G, kCols>(grads, dim, c0, s_seg[j], s_seg[j + 1], [&](uint32_t k) { return s_pos[k]; },
-                              gsum + static_cast<uint64_t>(first_u + j) * dim + c0);
+        run += chunk_heads;
     }
 }
 
@@ -1163,23 +1135,20 @@ int sort_bits(int64_t key_bound) {
 
 struct DedupLayout {
     int nblocks, hist_stride;
-    uint32_t nb_max;  // buckets the bucket dedup may use (0: it is not used for this n)
-    uint32_t ntiles;  // its histogram tiles
-    size_t keys_b, pos_a, pos_b, hist, heads, seg_start, seg_pos, tmp, bk_mat, bk_excl, bk_btot,
-        bk_start, bk_ucount, total;
+    uint32_t ng_max;  // groups the group dedup may use (0: it is not used for this n)
+    uint32_t ntiles;  // its tiles
+    size_t keys_b, pos_a, pos_b, hist, heads, seg_start, seg_pos, tmp, gd_off, gd_start, gd_ucount, total;
 };
 
-// The bucket dedup aims at kBucketMean keys per bucket (one LDS sort each) and is used up to
-// kBucketMaxN keys (beyond, buckets would average more than 256 keys: the radix sort then).
-constexpr int64_t kBucketMean = 24;
-constexpr int64_t kBucketMaxN = int64_t{1} << 21;
+// The group dedup is used up to kGdMaxN keys (kGdMaxTiles tiles of kGdTile).
+constexpr int64_t kGdMaxN = static_cast<int64_t>(kGdMaxTiles) * kGdTile;
 
 DedupLayout dedup_layout(int64_t n) {
     DedupLayout l{};
     l.nblocks = static_cast<int>(ceil_div(n, kTile));
-    if (n <= kBucketMaxN) {
-        l.nb_max = static_cast<uint32_t>(std::min<int64_t>(n / kBucketMean + 1, kBkMaxBuckets));
-        l.ntiles = static_cast<uint32_t>(ceil_div(n, kBkTile));
+    if (n <= kGdMaxN) {
+        l.ng_max = static_cast<uint32_t>(std::min<int64_t>(n / kGdMean + 1, kGdMaxGroups));
+        l.ntiles = static_cast<uint32_t>(ceil_div(n, kGdTile));
     }
     auto up = [](size_t x) { return (x + 255) & ~size_t{255}; };
     size_t off = 0;
@@ -1191,26 +1160,24 @@ DedupLayout dedup_layout(int64_t n) {
     l.heads = off; off += up(static_cast<size_t>(l.nblocks + 1) * 4);
     l.seg_start = off; off += up(static_cast<size_t>(n + 1) * 4);
     l.seg_pos = off; off += up(static_cast<size_t>(n) * 4);
-    if (l.nb_max > 0) {
+    if (l.ng_max > 0) {
         l.tmp = off; off += up(static_cast<size_t>(n) * 8);
-        l.bk_mat = off; off += up(static_cast<size_t>(l.nb_max) * l.ntiles * 4);
-        l.bk_excl = off; off += up(static_cast<size_t>(l.nb_max) * 4);
-        l.bk_btot = off; off += up(static_cast<size_t>(kBkMaxBuckets / kThreads) * 4);
-        l.bk_start = off; off += up(static_cast<size_t>(l.nb_max + 1) * 4);
-        l.bk_ucount = off; off += up(static_cast<size_t>(l.nb_max + 3) / 4 * 16);  // 16-byte reads
+        l.gd_off = off; off += up(static_cast<size_t>(l.ntiles) * (l.ng_max + 1) * 4);
+        l.gd_start = off; off += up(static_cast<size_t>(l.ng_max + 1) * 4);
+        l.gd_ucount = off; off += up(static_cast<size_t>(l.ng_max) * 4);
     }
     l.total = off;
     return l;
 }
 
-// Bucket shift for the bucket dedup: the smallest s whose buckets (key >> s) number at most
-// nb_max; -1 when the bucket dedup is not used (nb_max 0) or the low key bits below a bucket
+// Group shift for the group dedup: the smallest s whose groups (key >> s) number at most
+// ng_max; -1 when the group dedup is not used (ng_max 0) or the low key bits below a group
 // would not fit the 32 bits of a composite.
-int bucket_shift(int64_t key_bound, uint32_t nb_max) {
-    if (nb_max == 0) return -1;
+int group_shift(int64_t key_bound, uint32_t ng_max) {
+    if (ng_max == 0) return -1;
     const uint64_t top = static_cast<uint64_t>(key_bound - 1);
     int s = 0;
-    while (s < 63 && (top >> s) + 1 > nb_max) ++s;
+    while (s < 63 && (top >> s) + 1 > ng_max) ++s;
     return s <= 32 ? s : -1;
 }
 
@@ -1225,6 +1192,116 @@ extern "C" int me_dedup_workspace_size(int64_t n, size_t *bytes) {
     *bytes = dedup_layout(n).total;
     return ME_OK;
 }
+
+namespace me {
+namespace {
+
+// The segment plan both dedup paths leave for the sums: spos [n] (positions in sorted key
+// order), seg_start [n + 1] (first index into spos of each unique key, then n), seg_pos [n]
+// (first position of each unique key). Regions 256-byte aligned.
+struct PlanLayout {
+    size_t spos, seg_start, seg_pos, total;
+};
+
+PlanLayout plan_layout(int64_t n) {
+    auto up = [](size_t x) { return (x + 255) & ~size_t{255}; };
+    PlanLayout p{};
+    size_t off = 0;
+    p.spos = off; off += up(static_cast<size_t>(n) * 4);
+    p.seg_start = off; off += up(static_cast<size_t>(n + 1) * 4);
+    p.seg_pos = off; off += up(static_cast<size_t>(n) * 4);
+    p.total = off;
+    return p;
+}
+
+// The key half: unique keys, inverse, count and the segment plan (spos, seg_start, seg_pos).
+int dedup_keys_run(const int64_t *keys, int64_t n, int64_t key_bound, int64_t *uniq, int64_t *inv,
+                   int64_t *count, uint32_t *spos, uint32_t *seg_start, uint32_t *seg_pos,
+                   uint8_t *ws, const DedupLayout &l, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(l.nblocks)), block(kThreads);
+    const int shift = group_shift(key_bound, l.ng_max);
+    if (shift >= 0) {
+        // group dedup: per-tile grouping, per-group sort, the keys' emit
+        const uint32_t ng = static_cast<uint32_t>((static_cast<uint64_t>(key_bound - 1) >> shift) + 1);
+        uint64_t *tile_comp = reinterpret_cast<uint64_t *>(ws + l.keys_b);
+        uint64_t *comp = tile_comp + n;
+        uint64_t *tmp = reinterpret_cast<uint64_t *>(ws + l.tmp);
+        uint32_t *off = reinterpret_cast<uint32_t *>(ws + l.gd_off);
+        uint32_t *gstart = reinterpret_cast<uint32_t *>(ws + l.gd_start);
+        uint32_t *ucount = reinterpret_cast<uint32_t *>(ws + l.gd_ucount);
+        const uint64_t *k64 = reinterpret_cast<const uint64_t *>(keys);
+        hipLaunchKernelGGL(gd_tile, dim3(l.ntiles), block, 0, s, k64, n, shift, ng, tile_comp, off);
+        hipLaunchKernelGGL(gd_group, dim3(ng), block, 0, s, tile_comp, off, l.ntiles, ng, shift, n, comp,
+                           tmp, gstart, ucount);
+        hipLaunchKernelGGL(gd_emit, dim3(ng), block, 0, s, comp, gstart, ucount, ng, shift, uniq, inv, spos,
+                           seg_start, seg_pos, count);
+        return check_launch("me_dedup (keys, groups)");
+    }
+    // LSD radix sort of (key, position), 8 bits per pass, then the segments; the positions of
+    // the last pass land in spos
+    const int passes = (sort_bits(key_bound) + 7) / 8;
+    uint64_t *kb[2] = {reinterpret_cast<uint64_t *>(ws + l.keys_b),
+                       reinterpret_cast<uint64_t *>(ws + l.keys_b) + n};
+    uint32_t *pb[2];
+    pb[(passes - 1) & 1] = spos;
+    pb[passes & 1] = reinterpret_cast<uint32_t *>(ws + l.pos_a);
+    uint32_t *hist = reinterpret_cast<uint32_t *>(ws + l.hist);
+    uint32_t *heads = reinterpret_cast<uint32_t *>(ws + l.heads);
+    const uint64_t *kin = reinterpret_cast<const uint64_t *>(keys);
+    const uint32_t *pin = nullptr;
+    int cur = 0;
+    for (int p = 0; p < passes; ++p) {
+        const int sh = 8 * p;
+        hipLaunchKernelGGL(rs_hist, grid, block, 0, s, kin, n, sh, hist, l.nblocks, l.hist_stride);
+        hipLaunchKernelGGL(rs_scatter, grid, block, 0, s, kin, pin, kb[cur], pb[cur], n, sh, hist,
+                           l.hist_stride);
+        kin = kb[cur];
+        pin = pb[cur];
+        cur ^= 1;
+    }
+    const int st = check_launch("me_dedup (sort)");
+    if (st != ME_OK) return st;
+    hipLaunchKernelGGL(seg_count, grid, block, 0, s, kin, n, heads);
+    hipLaunchKernelGGL(seg_write, grid, block, 0, s, kin, pin, n, heads, l.nblocks, uniq, inv,
+                       seg_start, seg_pos, count);
+    return check_launch("me_dedup (keys, segments)");
+}
+
+// The gradient half: each unique key's fp32 sum of its rows, from the plan.
+int dedup_sums_run(const uint32_t *spos, const uint32_t *seg_start, const uint32_t *seg_pos,
+                   const int64_t *count, int64_t n, const void *grads, int grad_dtype, int32_t dim,
+                   float *gsum, hipStream_t s) {
+    // four columns per thread when every row start is aligned for the vector loads and stores
+    const size_t gsz = grad_dtype == ME_F32 ? 4 : 2;
+    const bool vec = dim % 4 == 0 && reinterpret_cast<uintptr_t>(grads) % (4 * gsz) == 0 &&
+                     reinterpret_cast<uintptr_t>(gsum) % 16 == 0;
+    const int64_t threads = n * (vec ? dim / 4 : dim);
+    ME_CHECK_ARG(threads < (int64_t{1} << 31), "n * dim = %lld too large for one call",
+                 (long long)(n * dim));
+    const dim3 sgrid(static_cast<unsigned>(ceil_div(threads, kThreads))), block(kThreads);
+    const uint32_t d = static_cast<uint32_t>(dim), sp = static_cast<uint32_t>(n);
+    if (grad_dtype == ME_F32) {
+        const float *g = static_cast<const float *>(grads);
+        if (vec)
+            hipLaunchKernelGGL((seg_sum<float, 4>), sgrid, block, 0, s, g, d, spos, seg_start, seg_pos, count,
+                               sp, gsum);
+        else
+            hipLaunchKernelGGL((seg_sum<float, 1>), sgrid, block, 0, s, g, d, spos, seg_start, seg_pos, count,
+                               sp, gsum);
+    } else {
+        const uint16_t *g = static_cast<const uint16_t *>(grads);
+        if (vec)
+            hipLaunchKernelGGL((seg_sum<uint16_t, 4>), sgrid, block, 0, s, g, d, spos, seg_start, seg_pos,
+                               count, sp, gsum);
+        else
+            hipLaunchKernelGGL((seg_sum<uint16_t, 1>), sgrid, block, 0, s, g, d, spos, seg_start, seg_pos,
+                               count, sp, gsum);
+    }
+    return check_launch("me_dedup (sums)");
+}
+
+}  // namespace
+}  // namespace me
 
 extern "C" int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const void *grads,
                         int grad_dtype, int32_t dim, int64_t *uniq, int64_t *inv, float *gsum,
@@ -1248,109 +1325,67 @@ extern "C" int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const
         return ME_ERR_WORKSPACE;
     }
     uint8_t *ws = static_cast<uint8_t *>(workspace);
-    uint64_t *kb[2] = {reinterpret_cast<uint64_t *>(ws + l.keys_b),
-                       reinterpret_cast<uint64_t *>(ws + l.keys_b) + n};
-    uint32_t *pb[2] = {reinterpret_cast<uint32_t *>(ws + l.pos_a),
-                       reinterpret_cast<uint32_t *>(ws + l.pos_b)};
-    uint32_t *hist = reinterpret_cast<uint32_t *>(ws + l.hist);
-    uint32_t *heads = reinterpret_cast<uint32_t *>(ws + l.heads);
+    uint32_t *spos = reinterpret_cast<uint32_t *>(ws + l.pos_b);
     uint32_t *seg_start = reinterpret_cast<uint32_t *>(ws + l.seg_start);
     uint32_t *seg_pos = reinterpret_cast<uint32_t *>(ws + l.seg_pos);
+    const int st = dedup_keys_run(keys, n, key_bound, uniq, inv, count, spos, seg_start, seg_pos, ws, l, s);
+    if (st != ME_OK || grads == nullptr) return st;
+    return dedup_sums_run(spos, seg_start, seg_pos, count, n, grads, grad_dtype, dim, gsum, s);
+}
 
-    const dim3 grid(static_cast<unsigned>(l.nblocks)), block(kThreads);
-    const int shift = bucket_shift(key_bound, l.nb_max);
-    const uint32_t *pin = nullptr;
-    if (shift >= 0) {
-        // bucket dedup: histograms, prefix, scatter, per-bucket sort, emit
-        const uint32_t nb = static_cast<uint32_t>((static_cast<uint64_t>(key_bound - 1) >> shift) + 1);
-        uint32_t *mat = reinterpret_cast<uint32_t *>(ws + l.bk_mat);
-        uint32_t *excl = reinterpret_cast<uint32_t *>(ws + l.bk_excl);
-        uint32_t *btot = reinterpret_cast<uint32_t *>(ws + l.bk_btot);
-        uint32_t *bstart = reinterpret_cast<uint32_t *>(ws + l.bk_start);
-        uint32_t *ucount = reinterpret_cast<uint32_t *>(ws + l.bk_ucount);
-        uint64_t *bkeys = kb[0], *comp = kb[1];
-        uint64_t *tmp = reinterpret_cast<uint64_t *>(ws + l.tmp);
-        uint32_t *bpos = pb[0], *spos = pb[1];
-        const uint64_t *k64 = reinterpret_cast<const uint64_t *>(keys);
-        const dim3 tgrid(l.ntiles), pgrid(static_cast<unsigned>(ceil_div(nb, kThreads))), bgrid(nb);
-        hipLaunchKernelGGL(bk_hist, tgrid, block, 0, s, k64, n, shift, nb, mat);
-        hipLaunchKernelGGL(bk_prefix, pgrid, block, 0, s, mat, nb, l.ntiles, excl, btot);
-        hipLaunchKernelGGL(bk_scatter, tgrid, block, 0, s, k64, n, shift, nb, mat, excl, btot, bkeys,
-                           bpos, bstart);
-        hipLaunchKernelGGL(bk_sort, bgrid, block, 0, s, bkeys, bpos, bstart, shift, comp, tmp, ucount);
-        const size_t gsz = grad_dtype == ME_F32 ? 4 : 2;
-        const bool vec4 = grads != nullptr && dim % 4 == 0 &&
-                          reinterpret_cast<uintptr_t>(grads) % (4 * gsz) == 0 &&
-                          reinterpret_cast<uintptr_t>(gsum) % 16 == 0;
-        const uint32_t d = grads != nullptr ? static_cast<uint32_t>(dim) : 0u;
-        if (grads == nullptr || grad_dtype == ME_F32) {
-            const float *g = static_cast<const float *>(grads);
-            if (vec4)
-                hipLaunchKernelGGL((bk_emit<float, 4>), bgrid, block, 0, s, comp, bstart, ucount, nb, shift,
-                                   g, d, uniq, inv, gsum, count);
-            else
-                hipLaunchKernelGGL((bk_emit<float, 1>), bgrid, block, 0, s, comp, bstart, ucount, nb, shift,
-                                   g, d, uniq, inv, gsum, count);
-        } else {
-            const uint16_t *g = static_cast<const uint16_t *>(grads);
-            if (vec4)
-                hipLaunchKernelGGL((bk_emit<uint16_t, 4>), bgrid, block, 0, s, comp, bstart, ucount, nb,
-                                   shift, g, d, uniq, inv, gsum, count);
-            else
-                hipLaunchKernelGGL((bk_emit<uint16_t, 1>), bgrid, block, 0, s, comp, bstart, ucount, nb,
-                                   shift, g, d, uniq, inv, gsum, count);
-        }
-        (void)spos;
-        return check_launch("me_dedup (buckets)");
-    } else {
-        // LSD radix sort of (key, position), 8 bits per pass, then the segments
-        const int passes = (sort_bits(key_bound) + 7) / 8;
-        const uint64_t *kin = reinterpret_cast<const uint64_t *>(keys);
-        int cur = 0;
-        for (int p = 0; p < passes; ++p) {
-            const int sh = 8 * p;
-            hipLaunchKernelGGL(rs_hist, grid, block, 0, s, kin, n, sh, hist, l.nblocks, l.hist_stride);
-            hipLaunchKernelGGL(rs_scatter, grid, block, 0, s, kin, pin, kb[cur], pb[cur], n, sh, hist,
-                               l.hist_stride);
-            kin = kb[cur];
-            pin = pb[cur];
-            cur ^= 1;
-        }
-        int st = check_launch("me_dedup (sort)");
-        if (st != ME_OK) return st;
-        hipLaunchKernelGGL(seg_count, grid, block, 0, s, kin, n, heads);
-        hipLaunchKernelGGL(seg_write, grid, block, 0, s, kin, pin, n, heads, l.nblocks, uniq, inv,
-                           seg_start, seg_pos, count);
-        st = check_launch("me_dedup (segments)");
-        if (st != ME_OK || grads == nullptr) return st;
+extern "C" int me_dedup_plan_size(int64_t n, size_t *bytes) {
+    ME_CHECK_ARG(bytes != nullptr, "bytes is null");
+    ME_CHECK_ARG(n >= 0 && n < (int64_t{1} << 31), "n out of range");
+    *bytes = plan_layout(n).total;
+    return ME_OK;
+}
+
+extern "C" int me_dedup_keys(const int64_t *keys, int64_t n, int64_t key_bound, int64_t *uniq,
+                             int64_t *inv, int64_t *count, void *plan, size_t plan_size,
+                             void *workspace, size_t workspace_size, void *stream) {
+    ME_CHECK_ARG(n >= 0 && n < (int64_t{1} << 31), "n out of range");
+    ME_CHECK_ARG(key_bound >= 1, "key_bound must be positive");
+    ME_CHECK_ARG(count != nullptr, "count is null");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) {
+        hipLaunchKernelGGL(write_zero_count, dim3(1), dim3(1), 0, s, count);
+        return check_launch("me_dedup_keys");
     }
-    // four columns per thread when every row start is aligned for the vector loads and stores
-    const size_t gsz = grad_dtype == ME_F32 ? 4 : 2;
-    const bool vec = dim % 4 == 0 && reinterpret_cast<uintptr_t>(grads) % (4 * gsz) == 0 &&
-                     reinterpret_cast<uintptr_t>(gsum) % 16 == 0;
-    const int64_t threads = n * (vec ? dim / 4 : dim);
-    ME_CHECK_ARG(threads < (int64_t{1} << 31), "n * dim = %lld too large for one call",
-                 (long long)(n * dim));
-    const dim3 sgrid(static_cast<unsigned>(ceil_div(threads, kThreads)));
-    const uint32_t d = static_cast<uint32_t>(dim), ns = static_cast<uint32_t>(n);
-    if (grad_dtype == ME_F32) {
-        const float *g = static_cast<const float *>(grads);
-        if (vec)
-            hipLaunchKernelGGL((seg_sum<float, 4>), sgrid, block, 0, s, g, d, pin, seg_start, seg_pos,
-                               count, ns, gsum);
-        else
-            hipLaunchKernelGGL((seg_sum<float, 1>), sgrid, block, 0, s, g, d, pin, seg_start, seg_pos,
-                               count, ns, gsum);
-    } else {
-        const uint16_t *g = static_cast<const uint16_t *>(grads);
-        if (vec)
-            hipLaunchKernelGGL((seg_sum<uint16_t, 4>), sgrid, block, 0, s, g, d, pin, seg_start,
-                               seg_pos, count, ns, gsum);
-        else
-            hipLaunchKernelGGL((seg_sum<uint16_t, 1>), sgrid, block, 0, s, g, d, pin, seg_start,
-                               seg_pos, count, ns, gsum);
+    ME_CHECK_ARG(keys && uniq && inv, "null tensor pointer");
+    const PlanLayout p = plan_layout(n);
+    if (plan == nullptr || plan_size < p.total) {
+        set_error("me_dedup_keys: plan of %zu bytes needed, got %zu", p.total, plan_size);
+        return ME_ERR_WORKSPACE;
     }
-    return check_launch("me_dedup (sums)");
+    const DedupLayout l = dedup_layout(n);
+    if (workspace == nullptr || workspace_size < l.total) {
+        set_error("me_dedup_keys: workspace of %zu bytes needed, got %zu", l.total, workspace_size);
+        return ME_ERR_WORKSPACE;
+    }
+    uint8_t *pl = static_cast<uint8_t *>(plan);
+    return dedup_keys_run(keys, n, key_bound, uniq, inv, count, reinterpret_cast<uint32_t *>(pl + p.spos),
+                          reinterpret_cast<uint32_t *>(pl + p.seg_start),
+                          reinterpret_cast<uint32_t *>(pl + p.seg_pos), static_cast<uint8_t *>(workspace), l,
+                          s);
+}
+
+extern "C" int me_dedup_sums(const void *plan, size_t plan_size, int64_t n, const int64_t *count,
+                             const void *grads, int grad_dtype, int32_t dim, float *gsum, void *stream) {
+    ME_CHECK_ARG(n >= 0 && n < (int64_t{1} << 31), "n out of range");
+    ME_CHECK_ARG(grad_dtype == ME_F32 || grad_dtype == ME_BF16, "grad dtype must be fp32 or bf16");
+    ME_CHECK_ARG(dim >= 1, "dim must be positive");
+    if (n == 0) return ME_OK;
+    ME_CHECK_ARG(count && grads && gsum, "null tensor pointer");
+    const PlanLayout p = plan_layout(n);
+    if (plan == nullptr || plan_size < p.total) {
+        set_error("me_dedup_sums: plan of %zu bytes needed, got %zu", p.total, plan_size);
+        return ME_ERR_WORKSPACE;
+    }
+    const uint8_t *pl = static_cast<const uint8_t *>(plan);
+    return dedup_sums_run(reinterpret_cast<const uint32_t *>(pl + p.spos),
+                          reinterpret_cast<const uint32_t *>(pl + p.seg_start),
+                          reinterpret_cast<const uint32_t *>(pl + p.seg_pos), count, n, grads, grad_dtype,
+                          dim, gsum, as_stream(stream));
 }
 
 extern "C" int me_sumsq(const float *x, int64_t n, float *out, int accumulate, void *workspace,

@@ -485,6 +485,44 @@ def _(keys, key_bound, grads):
     return outs
 
 
+def dedup_plan_bytes(n):
+    size = ctypes.c_size_t(0)
+    call("me_dedup_plan_size", n, ctypes.byref(size))
+    return size.value
+
+
+def dedup_keys(keys, key_bound):
+    """[uniq [n], inv [n], count [1], plan (uint8)]: the key half of dedup -- torch.unique(keys,
+    return_inverse=True) (micro_engram/rows.py:81) and the segment plan dedup_sums reads. Depends
+    only on the keys, so it can run before the gradients exist."""
+    dev = require_gpu(keys)
+    keys = keys.reshape(-1).long().contiguous()
+    n = keys.numel()
+    uniq = torch.empty(n, dtype=torch.int64, device=dev)
+    inv = torch.empty(n, dtype=torch.int64, device=dev)
+    count = torch.empty(1, dtype=torch.int64, device=dev)
+    plan = torch.empty(max(dedup_plan_bytes(n), 16), dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(dedup_workspace_bytes(n), 16), dtype=torch.uint8, device=dev)
+    call("me_dedup_keys", _p(keys), n, key_bound, _p(uniq), _p(inv), count.data_ptr(), plan.data_ptr(),
+         plan.numel(), ws.data_ptr(), ws.numel(), stream_of(dev))
+    return [uniq, inv, count, plan]
+
+
+def dedup_sums(plan, count, grads):
+    """fp32 [n, D]: row u = the index_add_ sum of the gradient rows of unique key u (rows.py:117-118),
+    from the plan and count of dedup_keys on the same n keys; rows past the count are unset."""
+    dev = require_gpu(plan, count, grads)
+    n = grads.shape[0]
+    grads = grads.reshape(n, grads.shape[-1] if grads.dim() >= 2 else 1)
+    if grads.dtype not in (torch.float32, torch.bfloat16):
+        grads = grads.float()
+    grads = grads.contiguous()
+    gsum = torch.empty((n, grads.shape[1]), dtype=torch.float32, device=dev)
+    call("me_dedup_sums", plan.data_ptr(), plan.numel(), n, count.data_ptr(), grads.data_ptr(),
+         dtype_code(grads), grads.shape[1], gsum.data_ptr(), stream_of(dev))
+    return gsum
+
+
 def sumsq(x, out=None, accumulate=False):
     """Sum of squares of an fp32 tensor into a device scalar (the squared gradient norm of
     RowTables.clip, micro_engram/rows.py:214-223)."""

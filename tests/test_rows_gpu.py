@@ -82,6 +82,34 @@ def test_dedup_empty():
     assert uniq.numel() == 0 and inv.numel() == 0 and gsum.shape == (0, 4)
 
 
+@pytest.mark.parametrize("n,bound,dim,dtype", [(196608, 79_691_776, 64, torch.float32),
+                                               (5000, 1 << 40, 16, torch.float32),
+                                               (4000, 300, 6, torch.bfloat16), (1, 5, 4, torch.float32)])
+def test_dedup_split_halves_bit_exact(n, bound, dim, dtype):
+    # the key half (unique keys, inverse, segment plan) run before the gradients exist, then the
+    # sums from the plan: the same unique keys, inverse and fp32 sums as the oracle's one call;
+    # bucket path (the workload's key range), radix path (40-bit keys), unaligned widths
+    g = torch.Generator().manual_seed(n + dim)
+    keys = torch.randint(0, bound, (n,), generator=g)
+    if n > 100:
+        keys[::5] = keys[1]
+    grads = (torch.randn(n, dim, generator=g) * torch.logspace(-3, 2, n).unsqueeze(1)).to(dtype)
+    uniq, inv, count, plan = ops.dedup_keys(keys.to(DEV), bound)
+    gsum = ops.dedup_sums(plan, count, grads.to(DEV))
+    c = int(count.item())
+    u, i, acc = oracle.dedup(keys.numpy(), grads.float().numpy())
+    assert c == len(u)
+    assert np.array_equal(uniq[:c].cpu().numpy(), u)
+    assert np.array_equal(inv.cpu().numpy(), i)
+    assert np.array_equal(gsum[:c].cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
+def test_dedup_split_halves_empty():
+    uniq, inv, count, plan = ops.dedup_keys(torch.zeros(0, dtype=torch.long, device=DEV), 10)
+    gsum = ops.dedup_sums(plan, count, torch.zeros(0, 4, device=DEV))
+    assert int(count.item()) == 0 and uniq.numel() == 0 and gsum.shape == (0, 4)
+
+
 def test_add_sparse_grad_merges_like_reference():
     # rows.py:137-147: earlier entries first, then unique + index_add_
     p = torch.zeros(50, 8, device=DEV)
