@@ -9,7 +9,9 @@ forward (fused hash + row gather, then the K/V projection + scalar_sqrt gate + r
 all inputs already in HBM. Prints one JSON line:
 
   value         forward tokens/s over the K timed steps: one replay of a HIP graph of the K
-                steps, wall clock, synchronised. Step k runs on prefill batch k % 16 of 16
+                steps, wall clock, synchronised, after ~0.25 s of untimed replays of the same
+                graph (an idle part needs ~0.1-0.2 s of load to reach its sustained clock; without
+                them a 20-step replay reads ~8 % slow). Step k runs on prefill batch k % 16 of 16
                 distinct seeded batches of this shape, so a step's gather meets caches that
                 hold other batches' rows
   roofline      the gather kernel (the metric's HBM figure): algorithmic bytes per launch /
@@ -17,11 +19,14 @@ all inputs already in HBM. Prints one JSON line:
                 16 batches captured as a HIP graph, replayed between HIP events on the replay
                 stream (the rocprofv3 kernel trace of this script's step sequence agrees).
                 copy_1gib_gbs: a 1 GiB device copy, the known-size kernel that calibrates the
-                HBM byte counters
+                HBM byte counters; copy_same_size: a device copy of the gather's output size
+                (25 MB read + 25 MB written), the cost of the same bytes with no hashing
   roofline_gate the K/V projection + gate + residual kernels: 4 * M * d FLOP per token / their
                 mean duration (graph replay, as above), against 2.5 PFLOP/s dense bf16
   serving_decode  a decode step of 256 one-token sequences on the same engram (hash_prev +
-                inject, the calls of the vLLM decoder layer), graph replay over 16 distinct steps
+                inject, the calls of the vLLM decoder layer), graph replay over 16 distinct steps;
+                its roofline: the step's algorithmic bytes (both projection weights, the tokens'
+                table rows, ids, hidden in and out) / its duration, against 8 TB/s
   roofline_update  the training-side sparse update of a batch of this shape (dedup of the
                 196,608 lookups + row-wise Adam with stochastic rounding on the touched rows),
                 algorithmic bytes / duration (graph replay) over 16 distinct batches
@@ -220,11 +225,29 @@ def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5):
                       f"added"}
 
 
+SETTLE_S = 0.25  # sustained replays before a timed one (the part's clock settles in ~0.1-0.2 s)
+
+
+def settle(graph, seconds=SETTLE_S):
+    """Replays `graph` back to back for about `seconds` (untimed, synchronised at the end). An
+    MI355X that has idled runs its first milliseconds of work measurably slower than under
+    sustained load (a 20-step replay right after a pause: ~290-305 us per step; after 0.2 s of
+    replays: ~275 us, the same as a 50-step replay), so a timed replay is taken at the
+    sustained operating point a serving loop runs at."""
+    t0 = time.perf_counter()
+    while True:
+        graph.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 def replay_ms(fns, reps):
     """Mean duration in ms of one call of the sequence `fns`: `reps` rounds of the calls
     captured in one HIP graph and replayed between two HIP events on the replay stream
-    (consecutive kernels of a graph start back to back, so the events add nothing per call).
-    Returns the mean per call of the sequence (total / (reps * len(fns)))."""
+    (consecutive kernels of a graph start back to back, so the events add nothing per call),
+    after the graph has settled the part's clock. Returns the mean per call of the sequence
+    (total / (reps * len(fns)))."""
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -236,8 +259,7 @@ def replay_ms(fns, reps):
             for _ in range(reps):
                 for fn in fns:
                     fn()
-        graph.replay()
-        torch.cuda.synchronize()
+        settle(graph, 0.1)
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(side)
         graph.replay()
@@ -248,7 +270,8 @@ def replay_ms(fns, reps):
 
 def graph_step_ms(step, n_steps):
     """Wall-clock ms per call of step(k), k = 0 .. n_steps-1 captured as one HIP graph and
-    replayed once (synchronised on both sides), after an eager warm-up of each call."""
+    replayed once (synchronised on both sides), after an eager warm-up of each call and the
+    graph's settle replays."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -259,8 +282,7 @@ def graph_step_ms(step, n_steps):
         with torch.cuda.graph(graph, stream=side):
             for k in range(n_steps):
                 step(k)
-        graph.replay()
-        torch.cuda.synchronize()
+        settle(graph, 0.1)
         t0 = time.perf_counter()
         graph.replay()
         torch.cuda.synchronize()
@@ -392,7 +414,8 @@ def main():
         torch.cuda.synchronize()
         # The K steps are captured once as a HIP graph (the serving idiom: every op is graph
         # safe, no host synchronisation, shapes fixed) and the timed region is one replay of
-        # it, synchronised on both sides.
+        # it, synchronised on both sides, after untimed replays have brought the part to its
+        # sustained clock (settle).
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(stream)
@@ -400,8 +423,7 @@ def main():
             with torch.cuda.graph(graph, stream=side):
                 for k in range(args.steps):
                     step(k)
-            graph.replay()
-            torch.cuda.synchronize()
+            settle(graph)
             t0 = time.perf_counter()
             graph.replay()
             torch.cuda.synchronize()
@@ -428,6 +450,16 @@ def main():
         decode_ms = replay_ms([(lambda k=k: decode(k)) for k in range(CYCLE)], 2)
         decode_tokens = dsteps[0][0].shape[0]
         del dsteps
+
+        # A plain device copy of the gather's output size (each launch on other buffers, as the
+        # gather meets rows no earlier launch read): what moving the same bytes costs on this
+        # part with no hashing and no random reads
+        gbytes_out = T * len(eng.tables) * eng.engram_dim * eng.tables[0].weight.element_size()
+        ring = torch.empty(2 * CYCLE * gbytes_out, dtype=torch.uint8, device=dev)
+        views = [(ring[2 * k * gbytes_out:(2 * k + 1) * gbytes_out],
+                  ring[(2 * k + 1) * gbytes_out:(2 * k + 2) * gbytes_out]) for k in range(CYCLE)]
+        copy_same_ms = replay_ms([(lambda k=k: views[k][1].copy_(views[k][0])) for k in range(CYCLE)], 2)
+        del views, ring
 
         # The sparse update (dedup + row-wise Adam with stochastic rounding) of the same
         # batch shape, over the same cycle of distinct batches; it writes the tables, so it
@@ -472,6 +504,13 @@ def main():
     gate_flop = 4.0 * M * d * T
     gate_tflops = gate_flop / (gate_ms * 1e-3) / 1e12
 
+    # decode step: algorithmic bytes = both projection weights + the 256 tokens' table rows, ids,
+    # hidden read and output written (the weights dominate: 33 MB)
+    n_dec = decode_tokens
+    decode_bytes = (2 * d * M * esize + n_dec * len(eng.table_rows) * eng.engram_dim * esize
+                    + n_dec * 4 * 4 + 2 * n_dec * d * esize)
+    decode_gbs = decode_bytes / (decode_ms * 1e-3) / 1e9
+
     dedup_b, adam_b = update_bytes(n_lookups, n_uniq, eng.engram_dim, esize)
     update_gbs = (dedup_b + adam_b) / ((dedup_ms + adam_ms) * 1e-3) / 1e9
     result = {
@@ -507,6 +546,8 @@ def main():
             "canon_read": canon_read,
             "mean_ms": gather_ms,
             "copy_1gib_gbs": copy_gbs,
+            "copy_same_size_ms": copy_same_ms,
+            "copy_same_size_gbs": 2.0 * gbytes_out / (copy_same_ms * 1e-3) / 1e9,
         },
         "roofline_gate": {
             "kernel": "K/V projection + gate + residual (gate224_kernel key + value passes on 256 x 224 "
@@ -545,6 +586,8 @@ def main():
                         "int32 ids with -1), hidden 5376 bf16: hash_prev + inject per step",
             "step_us": decode_ms * 1e3,
             "tokens_per_s": decode_tokens / (decode_ms * 1e-3),
+            "roofline": {"bound": "hbm", "bytes_per_step": decode_bytes, "achieved": decode_gbs,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": decode_gbs / HBM_PEAK_GBS},
         },
         "tiny_forward": tiny,
         "two_engram_canon": two,
