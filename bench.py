@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="seconds of untimed replays before each timed one (0 under a profiler that "
+                         "counts every dispatch)")
     return ap.parse_args()
 
 
@@ -226,14 +229,16 @@ def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5):
 
 
 SETTLE_S = 0.25  # sustained replays before a timed one (the part's clock settles in ~0.1-0.2 s)
+_SETTLE = [SETTLE_S]  # the run's setting (--settle caps every settle)
 
 
-def settle(graph, seconds=SETTLE_S):
+def settle(graph, seconds=None):
     """Replays `graph` back to back for about `seconds` (untimed, synchronised at the end). An
     MI355X that has idled runs its first milliseconds of work measurably slower than under
     sustained load (a 20-step replay right after a pause: ~290-305 us per step; after 0.2 s of
     replays: ~275 us, the same as a 50-step replay), so a timed replay is taken at the
     sustained operating point a serving loop runs at."""
+    seconds = _SETTLE[0] if seconds is None else min(seconds, _SETTLE[0])
     t0 = time.perf_counter()
     while True:
         graph.replay()
@@ -375,6 +380,7 @@ def measure_two_engram(dev, steps=3):
 
 def main():
     args = parse()
+    _SETTLE[0] = max(args.settle, 0.0)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the engram path here has no multi-GPU mode "
               f"(asked for --gpus {args.gpus}). Run with --gpus 1.", file=sys.stderr)

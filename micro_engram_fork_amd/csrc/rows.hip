@@ -1116,6 +1116,101 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     if (RW && sub == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
 }
 
+// Rows wider than 64 lanes x C columns (the dense key / value weights: 1,536 columns): one wave
+// per row walking nb blocks of 64 x C columns, the same arithmetic and noise as adam_rows_vec per
+// block. The lazy skip and the row-wise second moment need the whole row's gradient first: a
+// pass over its blocks before the update pass (which loads them again).
+template <int C, bool PB, bool RW>
+__global__ __launch_bounds__(kThreads) void adam_rows_wide(const AdamArgs a) {
+    __shared__ AdamTable s_t[kAdamTables];
+    const int tid = threadIdx.x;
+    {
+        const uint64_t *src = reinterpret_cast<const uint64_t *>(a.t);
+        uint64_t *dst = reinterpret_cast<uint64_t *>(s_t);
+        const int words = a.n_tables * static_cast<int>(sizeof(AdamTable) / 8);
+        for (int w = tid; w < words; w += kThreads) dst[w] = src[w];
+    }
+    __syncthreads();
+    const int lane = tid & 63;
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (tid >> 6);
+    if (slot >= a.total) return;
+    int lo = 0, hi = a.n_tables - 1;  // last table whose first slot is <= slot
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_t[mid].first <= slot) lo = mid; else hi = mid - 1;
+    }
+    const AdamTable &t = s_t[lo];
+    const int D = a.dim, nb = D / (64 * C);
+    const int64_t i = slot - t.first;
+    const int64_t row = *as_global(t.rows + i);
+    const uint8_t *grow = reinterpret_cast<const uint8_t *>(t.grads);
+    float v_row = 0.f, denom_row = 0.f;
+    if (RW || a.lazy) {
+        bool any = false;
+        float gsq = 0.f;
+        for (int b = 0; b < nb; ++b) {
+            float g[C];
+            load_cols<C, false>(grow, i * D + b * 64 * C + lane * C, g);
+#pragma unroll
+            for (int e = 0; e < C; ++e) {
+                any |= g[e] != 0.f;
+                gsq += g[e] * g[e];
+            }
+        }
+        // lazy: a row whose gradient is all zero is skipped entirely (optim.py:92-95)
+        if (a.lazy && __ballot(any) == 0ull) return;
+        if constexpr (RW) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) gsq += __shfl_xor(gsq, off, 64);
+            const float v0 = *as_global(reinterpret_cast<const float *>(t.exp_avg_sq) + row);
+            v_row = fmaf(gsq / static_cast<float>(D), a.one_minus_beta2, v0 * a.beta2);
+            denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
+        }
+    }
+    for (int b = 0; b < nb; ++b) {
+        const int c0 = b * 64 * C + lane * C;
+        const int64_t e0 = row * D + c0;
+        float g[C], p[C], m[C], v[C];
+        load_cols<C, false>(grow, i * D + c0, g);
+        load_cols<C, PB>(t.param, e0, p);
+        load_cols<C, PB>(t.exp_avg, e0, m);
+        if constexpr (!RW) {
+            if (a.sq_bf16)
+                load_cols<C, true>(t.exp_avg_sq, e0, v);
+            else
+                load_cols<C, false>(t.exp_avg_sq, e0, v);
+        }
+#pragma unroll
+        for (int e = 0; e < C; ++e) {
+            if (a.has_decay) p[e] = p[e] * a.decay;
+            m[e] = fmaf(g[e], a.one_minus_beta1, m[e] * a.beta1);
+            float denom = denom_row;
+            if constexpr (!RW) {
+                v[e] = v[e] * a.beta2 + a.one_minus_beta2 * g[e] * g[e];
+                denom = sqrtf(v[e]) / t.sqrt_bc2 + a.eps;
+            }
+            p[e] = p[e] + (t.neg_lr_bc1 * m[e]) / denom;
+        }
+        uint32_t nz[C];
+#pragma unroll
+        for (int e = 0; e < C; ++e) nz[e] = 0u;
+        if constexpr (!RW) {
+            if (a.sq_bf16) {
+                if (a.sr) sr_noise_cols<C>(a.seed, t.step, t.stream_id, row, c0, 2, nz);
+                store_cols<C, true>(t.exp_avg_sq, e0, v, a.sr, nz);
+            } else {
+                store_cols<C, false>(t.exp_avg_sq, e0, v, a.sr, nz);
+            }
+        }
+        const bool rnd = PB && a.sr;
+        if (rnd) sr_noise_cols<C>(a.seed, t.step, t.stream_id, row, c0, 0, nz);
+        store_cols<C, PB>(t.param, e0, p, a.sr, nz);
+        if (rnd) sr_noise_cols<C>(a.seed, t.step, t.stream_id, row, c0, 1, nz);
+        store_cols<C, PB>(t.exp_avg, e0, m, a.sr, nz);
+    }
+    if (RW && lane == 0) *as_global(reinterpret_cast<float *>(t.exp_avg_sq) + row) = v_row;
+}
+
 // Standalone stochastic rounding of n fp32 values; element i uses the noise of (row i / 4096,
 // column i % 4096) of stream `stream_id` at step `step`, array 0.
 __global__ __launch_bounds__(kThreads) void sr_convert(const float *x, int64_t n, uint16_t *out,
@@ -1525,7 +1620,31 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
         };
         hipStream_t s = as_stream(stream);
         const int lpr8 = fits(8), lpr4 = lpr8 ? 0 : fits(4);
-        if (lpr8 || lpr4) {
+        // rows of whole 64-lane blocks of 8 columns (wider than one pass of adam_rows_vec)
+        const bool wide = !lpr8 && !lpr4 && dim % 512 == 0 &&
+                          [&] {
+                              const uintptr_t pal = 16, val = a.rowwise ? 4 : 16;
+                              for (int q = 0; q < nk; ++q) {
+                                  const AdamTable &t = a.t[q];
+                                  if (reinterpret_cast<uintptr_t>(t.param) % pal != 0 ||
+                                      reinterpret_cast<uintptr_t>(t.exp_avg) % pal != 0 ||
+                                      reinterpret_cast<uintptr_t>(t.exp_avg_sq) % val != 0 ||
+                                      reinterpret_cast<uintptr_t>(t.grads) % 16 != 0)
+                                      return false;
+                              }
+                              return true;
+                          }();
+        if (wide) {
+            const dim3 grid(static_cast<unsigned>(ceil_div(total, kThreads / 64)));
+            if (a.param_bf16 && a.rowwise)
+                hipLaunchKernelGGL((adam_rows_wide<8, true, true>), grid, dim3(kThreads), 0, s, a);
+            else if (a.param_bf16)
+                hipLaunchKernelGGL((adam_rows_wide<8, true, false>), grid, dim3(kThreads), 0, s, a);
+            else if (a.rowwise)
+                hipLaunchKernelGGL((adam_rows_wide<8, false, true>), grid, dim3(kThreads), 0, s, a);
+            else
+                hipLaunchKernelGGL((adam_rows_wide<8, false, false>), grid, dim3(kThreads), 0, s, a);
+        } else if (lpr8 || lpr4) {
             const int lpr = lpr8 ? lpr8 : lpr4;
             const int64_t per_block = (64 / lpr) * (kThreads / 64);
             const dim3 grid(static_cast<unsigned>(ceil_div(total, per_block)));

@@ -153,7 +153,8 @@ def test_stochastic_bf16_unbiased():
         assert abs(float(out.mean()) - x) < 2e-5
 
 
-def _adam_case(dtype, rowwise, R=300, D=64, n=120, steps=3, wd=0.0, sr=True, seed=123, lazy=True):
+def _adam_case(dtype, rowwise, R=300, D=64, n=120, steps=3, wd=0.0, sr=True, seed=123, lazy=True,
+               zero_rows=True):
     g = torch.Generator().manual_seed(R + D)
     init = (torch.randn(R, D, generator=g) * 0.02).to(dtype)
     p_gpu = init.clone().to(DEV)
@@ -164,7 +165,8 @@ def _adam_case(dtype, rowwise, R=300, D=64, n=120, steps=3, wd=0.0, sr=True, see
     for step in range(1, steps + 1):
         rows = torch.randperm(R, generator=g)[:n].sort().values
         grads = torch.randn(n, D, generator=g) * 1e-3
-        grads[::7] = 0  # untouched rows inside the list
+        if zero_rows:
+            grads[::7] = 0  # untouched rows inside the list
         ops.sparse_adam([p_gpu], [m_gpu], [v_gpu], [rows.to(DEV)], [grads.to(DEV)], [step], [3],
                         lr=5e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd, rowwise=rowwise,
                         lazy=lazy, stochastic_rounding=sr, seed=seed)
@@ -204,6 +206,23 @@ def test_sparse_adam_kernel_shapes_match_oracle(D, rowwise):
     # 8 columns per lane (D = 8, 128, 512: 1, 16, 64 lanes per row), 4 per lane (D = 4), one
     # wave per row (D = 12)
     (p, m, v), (pr, mr, vr) = _adam_case(torch.bfloat16, rowwise, D=D, R=97, n=40)
+    _assert_bf16_close(p, pr, frac=1e-2)
+    _assert_bf16_close(m, mr, frac=1e-2)
+    if rowwise:
+        assert torch.allclose(v, vr, rtol=1e-6, atol=0)
+    else:
+        _assert_bf16_close(v, vr, frac=1e-2)
+
+
+@pytest.mark.parametrize("D", [1024, 1536])
+@pytest.mark.parametrize("rowwise", [True, False])
+@pytest.mark.parametrize("lazy", [True, False])
+def test_sparse_adam_wide_rows_match_oracle(D, rowwise, lazy):
+    # rows wider than one 64-lane pass (the dense key / value weights: 1,536 columns), one wave
+    # per row over 512-column blocks; lazy=False (the dense AdamW of the trainer) with every
+    # listed row touched, as the oracle's lazy step then updates the same rows
+    (p, m, v), (pr, mr, vr) = _adam_case(torch.bfloat16, rowwise, D=D, R=53, n=30, lazy=lazy,
+                                         zero_rows=lazy)
     _assert_bf16_close(p, pr, frac=1e-2)
     _assert_bf16_close(m, mr, frac=1e-2)
     if rowwise:
