@@ -295,15 +295,17 @@ extern "C" int me_kv_proj(const void *mem, int64_t n, int64_t mem_dim, const voi
     a.mem_bytes = static_cast<uint32_t>(n * mem_dim * es);
     a.w_bytes = static_cast<uint32_t>(model_dim * mem_dim * es);
     hipStream_t s = as_stream(stream);
-    // Tiles (measured on MI355X at model dim 5376, mem dim 1536): each CU moves its operands at
-    // a rate of its own, so small batches want about as many workgroups as the part has CUs --
-    // up to 64 tokens 64 x 96, up to 256 tokens 128 x 96 (a 256-token decode step: 224
-    // workgroups, 19.6 us; 128 x 192 or 256 x 96 tiles: 27-30 us) -- and larger ones the
-    // bigger 128 x 192 tile, which moves fewer bytes per MFMA (2048 tokens: 104 us against 121).
-    // fp32: 128 x 128 (MFMA-bound).
+    // Tiles (measured on MI355X at model dim 5376, mem dim 1536, bf16): small batches are
+    // bound by how many bytes each CU keeps in flight from L2, so they take tiles whose ring
+    // leaves room for two workgroups per CU (four slots of 128-byte slabs) -- up to 64 tokens
+    // 32 x 96 (10.8 us against 12.8 us with one 64 x 96 workgroup per CU), up to 256 tokens
+    // 64 x 96 (a 256-token decode step's projection: 15.8-16.0 us against 17.8 us with 128 x 96
+    // and a five-slot ring; 128 x 64, 64 x 128 and 32 x 96 there: 17-20 us) -- and larger batches
+    // the 128 x 192 tile, which moves the fewest bytes per MFMA (512 tokens 26.8 us, 1024 tokens
+    // 50 us). fp32: 128 x 128 (MFMA-bound).
     if (dtype == ME_BF16) {
-        if (n <= 64) return launch<uint16_t, 2, 3, 5>(a, s);
-        if (n <= 256) return launch<uint16_t, 4, 3, 5>(a, s);
+        if (n <= 64) return launch<uint16_t, 1, 3, 4>(a, s);
+        if (n <= 256) return launch<uint16_t, 2, 3, 4>(a, s);
         return launch<uint16_t, 4, 6, 4>(a, s);
     }
     return launch<float, 4, 4, 5>(a, s);
