@@ -8,14 +8,14 @@
 //   alpha = sigmoid(s); out = x + round_H(alpha * V * keep)
 //
 // The fused two-pass kernel (gate.hip) computes K and V tile by tile on 256-token MFMA tiles:
-// below a few thousand tokens it has fewer tiles than the part has CUs, and one tile's K loop
-// sets its time (a 512-token batch: ~83 us). For such batches the projections run as
-// one plain GEMM of the memory vectors against the stacked [W_K; W_V] (the library BLAS
-// spreads small M over every CU), and this kernel does the rest in one pass over the rows:
-// one 256-thread workgroup per token (a decode batch of 256 tokens fills the part's 256 CUs),
-// 8 columns per thread per step with 16-byte loads, the three sums sum K^2, sum x (1 + dq)
-// (1 + dk) K and sum x^2 reduced across the workgroup, the gate, then x + round_H(alpha V)
-// written with 16-byte stores (the row is re-read from the cache).
+// below about a thousand tokens it has fewer tiles than the part has CUs, and one tile's K loop
+// sets its time. For such batches the projections run in the few-token GEMM (me_kv_proj,
+// proj.hip) and this kernel does the rest in one pass over the rows: one 256-thread workgroup
+// per token (a decode batch of 256 tokens fills the part's 256 CUs), 8 columns per thread per
+// step with 16-byte loads of hidden, K and V issued together (V and hidden stay in registers
+// for the output, so the row's only memory round trip is before the reduction), the three sums
+// sum K^2, sum x (1 + dq) (1 + dk) K and sum x^2 reduced across the workgroup, the gate, then
+// x + round_H(alpha V) written with 16-byte stores.
 #include "me_common.h"
 
 #include <cmath>
@@ -25,6 +25,7 @@ namespace {
 
 constexpr int kThreads = 256;  // one token per workgroup
 constexpr int kLaneCols = 8;
+constexpr int kKeep = 3;      // steps kept in registers: rows up to 3 * 2048 columns
 
 struct RowArgs {
     const uint8_t *hidden;  // [n, d] of H
@@ -102,10 +103,20 @@ __global__ __launch_bounds__(kThreads) void gate_rows_kernel(const RowArgs a) {
     const uint8_t *kr = a.k + n * a.kv_stride * static_cast<int64_t>(sizeof(T));
     const uint8_t *vr = a.v + n * a.kv_stride * static_cast<int64_t>(sizeof(T));
     float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
-    for (int64_t j = static_cast<int64_t>(tid) * kLaneCols; j < a.d; j += kThreads * kLaneCols) {
+    // the row's hidden and V values of the first kKeep steps stay in registers for the output
+    float xk[kKeep][kLaneCols], vk[kKeep][kLaneCols];
+    int it = 0;
+    for (int64_t j = static_cast<int64_t>(tid) * kLaneCols; j < a.d; j += kThreads * kLaneCols, ++it) {
         float xv[kLaneCols], kv[kLaneCols], w[kLaneCols];
         load8<H>(x + j * sizeof(H), xv);
         load8<T>(kr + j * sizeof(T), kv);
+#pragma unroll
+        for (int q = 0; q < kKeep; ++q)
+            if (q == it) {
+#pragma unroll
+                for (int e = 0; e < kLaneCols; ++e) xk[q][e] = xv[e];
+                load8<T>(vr + j * sizeof(T), vk[q]);
+            }
         if (a.q_delta != nullptr) {
             float qd[kLaneCols], kd[kLaneCols];
             if (a.scale_bf16) {
@@ -164,10 +175,22 @@ __global__ __launch_bounds__(kThreads) void gate_rows_kernel(const RowArgs a) {
     }
     if (a.keep != nullptr && a.keep[n] == 0) alpha = 0.f;
     uint8_t *o = a.out + n * a.d * static_cast<int64_t>(sizeof(H));
-    for (int64_t j = static_cast<int64_t>(tid) * kLaneCols; j < a.d; j += kThreads * kLaneCols) {
+    it = 0;
+    for (int64_t j = static_cast<int64_t>(tid) * kLaneCols; j < a.d; j += kThreads * kLaneCols, ++it) {
         float xv[kLaneCols], vv[kLaneCols], ov[kLaneCols];
-        load8<H>(x + j * sizeof(H), xv);
-        load8<T>(vr + j * sizeof(T), vv);
+        if (it < kKeep) {
+#pragma unroll
+            for (int q = 0; q < kKeep; ++q)
+                if (q == it)
+#pragma unroll
+                    for (int e = 0; e < kLaneCols; ++e) {
+                        xv[e] = xk[q][e];
+                        vv[e] = vk[q][e];
+                    }
+        } else {  // rows wider than kKeep steps: the rest is read again
+            load8<H>(x + j * sizeof(H), xv);
+            load8<T>(vr + j * sizeof(T), vv);
+        }
 #pragma unroll
         for (int e = 0; e < kLaneCols; ++e) ov[e] = xv[e] + round_to<H>(alpha * vv[e]);
         store8<H>(o + j * sizeof(H), ov);
