@@ -581,16 +581,25 @@ __global__ __launch_bounds__(kThreads) void gd_group(const uint64_t *tile_comp, 
             const uint32_t j = sub(c);
             const uint32_t blo = s_sb[j], bhi = s_sb[j + 1];
             uint32_t rank = 0, same = 0;
-            for (uint32_t m = blo; m < bhi; m += 4) {
+            auto count = [&](uint64_t dd) {
+                const uint32_t dk = static_cast<uint32_t>(dd >> 32), dp = static_cast<uint32_t>(dd);
+                rank += dk < ck ? 1u : 0u;
+                same += (dk == ck && dp < cp) ? 1u : 0u;
+            };
+            uint32_t m = blo;
+            for (; m + 16 <= bhi; m += 16) {  // a hot key's repeats: sixteen reads in flight
+                uint64_t d[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) d[q] = s_b[m + q];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) count(d[q]);
+            }
+            for (; m < bhi; m += 4) {
                 uint64_t d[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) d[q] = s_b[m + q < bhi ? m + q : k];  // k: never less
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t dk = static_cast<uint32_t>(d[q] >> 32), dp = static_cast<uint32_t>(d[q]);
-                    rank += dk < ck ? 1u : 0u;
-                    same += (dk == ck && dp < cp) ? 1u : 0u;
-                }
+                for (int q = 0; q < 4; ++q) count(d[q]);
             }
             rank += same;
             s_a[blo + rank] = c;  // s_a is free again: every composite is in s_b
