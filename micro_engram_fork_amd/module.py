@@ -388,8 +388,12 @@ class MicroEngram(nn.Module):
     def inject(self, hidden, idx, keep=None):
         """hidden + gated memory of the rows `idx` (module.py:228-261); keep: optional [N] bool,
         False leaves that token unchanged. Returns a new tensor."""
-        mem = self._mem_grad(idx) if self._needs_grad(hidden) else self._mem(idx)
-        return self._gate(hidden, mem, keep)
+        if not self._needs_grad(hidden):
+            return self._gate(hidden, self._mem(idx), keep)
+        from .rows import key_plans_after
+
+        with key_plans_after():  # the row dedup's key plan is issued behind the gate
+            return self._gate(hidden, self._mem_grad(idx), keep)
 
     def forward(self, hidden, input_ids, position_ids=None):
         """inject(hidden, hash_ids(input_ids, position_ids)) (module.py:263-265); without
@@ -413,10 +417,28 @@ class MicroEngram(nn.Module):
         return self._gate(hidden, mem, keep)
 
     # ------------------------------------------------------------------------- gate statistics
+    # gate tensors kept before they are folded into the running sums
+    _GATE_KEEP = 32
+
     def _record_gate(self, alpha):
-        """Accumulates (sum of alpha, count, count of alpha > 0.99) on the device, no host sync
-        (module.py:268-274)."""
-        a = alpha.detach().float()
+        """Records the step's gates for (sum of alpha, count, count of alpha > 0.99)
+        (module.py:268-274): the tensor is kept and reduced on the device when pop_gate_stats
+        reads the sums or every _GATE_KEEP records, so a training forward -- whose host issue
+        time bounds it -- pays no launches for it; no host sync either way."""
+        pending = self.__dict__.setdefault("_gate_pending", [])
+        a = alpha.detach()
+        if pending and pending[0].device != a.device:
+            self._fold_gate_stats()
+        pending.append(a)
+        if len(pending) >= self._GATE_KEEP:
+            self._fold_gate_stats()
+
+    def _fold_gate_stats(self):
+        pending = self.__dict__.get("_gate_pending")
+        if not pending:
+            return
+        a = torch.cat([t.reshape(-1).float() for t in pending])
+        pending.clear()
         stats = getattr(self, "_gate_stats", None)
         if stats is None or stats.device != a.device:
             stats = torch.zeros(3, device=a.device)
@@ -425,6 +447,7 @@ class MicroEngram(nn.Module):
 
     def pop_gate_stats(self):
         """(mean gate, fraction of tokens with gate > 0.99) since the last call, or None."""
+        self._fold_gate_stats()
         stats = getattr(self, "_gate_stats", None)
         self._gate_stats = None
         if stats is None or stats[1] == 0:

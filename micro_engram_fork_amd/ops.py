@@ -7,6 +7,7 @@ shape-only functions with no host synchronisation (the reference's own custom-op
 micro_engram/train/vendor/op_registry.py:40-67). CPU tensors raise: there is no CPU path.
 """
 import ctypes
+import functools
 from typing import List, Optional, Sequence
 
 import torch
@@ -30,19 +31,24 @@ def require_gpu(*tensors):
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        d = t.device
+        if d == dev:
+            continue
+        if d.type != "cuda":
             raise RuntimeError(
                 f"[micro_engram] the engram path runs only on the GPU (HIP kernels); got a tensor on "
-                f"{t.device}. Move the engram and its inputs to a GPU.")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise RuntimeError(f"[micro_engram] tensors on different devices: {dev} and {t.device}")
+                f"{d}. Move the engram and its inputs to a GPU.")
+        if dev is not None:
+            raise RuntimeError(f"[micro_engram] tensors on different devices: {dev} and {d}")
+        dev = d
     return dev
 
 
 def stream_of(device):
-    return torch.cuda.current_stream(device).cuda_stream
+    """Raw handle of the current stream on `device` (a cuda torch.device): one C call, where
+    torch.cuda.current_stream resolves the device and builds a Stream object each time."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def _p(t):
@@ -443,6 +449,7 @@ def library_loaded():
 
 
 # ------------------------------------------------------------------------- training side
+@functools.lru_cache(maxsize=64)
 def dedup_workspace_bytes(n):
     size = ctypes.c_size_t(0)
     call("me_dedup_workspace_size", n, ctypes.byref(size))
@@ -485,6 +492,7 @@ def _(keys, key_bound, grads):
     return outs
 
 
+@functools.lru_cache(maxsize=64)
 def dedup_plan_bytes(n):
     size = ctypes.c_size_t(0)
     call("me_dedup_plan_size", n, ctypes.byref(size))
@@ -498,9 +506,8 @@ def dedup_keys(keys, key_bound):
     dev = require_gpu(keys)
     keys = keys.reshape(-1).long().contiguous()
     n = keys.numel()
-    uniq = torch.empty(n, dtype=torch.int64, device=dev)
-    inv = torch.empty(n, dtype=torch.int64, device=dev)
-    count = torch.empty(1, dtype=torch.int64, device=dev)
+    ints = torch.empty(2 * n + 1, dtype=torch.int64, device=dev)  # three outputs, one allocation
+    uniq, inv, count = ints[:n], ints[n:2 * n], ints[2 * n:]
     plan = torch.empty(max(dedup_plan_bytes(n), 16), dtype=torch.uint8, device=dev)
     ws = torch.empty(max(dedup_workspace_bytes(n), 16), dtype=torch.uint8, device=dev)
     call("me_dedup_keys", _p(keys), n, key_bound, _p(uniq), _p(inv), count.data_ptr(), plan.data_ptr(),
@@ -566,23 +573,37 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
         return
     dim = params[0].shape[1]
     pdt = params[0].dtype
+    f32, i64 = torch.float32, torch.int64
+    # one pass: check every table's tensors (the kernel trusts these shapes) and collect the
+    # pointers; rows and grads that are not contiguous are copied (kept alive in `held`)
+    held, pp, mp, vp, rp, gp, counts = [], [], [], [], [], [], []
     for p, m, v, r, g in zip(params, exp_avgs, exp_avg_sqs, rows, grads):
-        if p.dim() != 2 or p.shape[1] != dim or p.dtype != pdt or not p.is_contiguous():
+        shape = p.shape
+        if len(shape) != 2 or shape[1] != dim or p.dtype != pdt or not p.is_contiguous():
             raise ValueError("[micro_engram] sparse_adam: tables must be contiguous [rows, D] of one dtype")
-        if m.shape != p.shape or m.dtype != pdt or not m.is_contiguous():
+        if m.shape != shape or m.dtype != pdt or not m.is_contiguous():
             raise ValueError("[micro_engram] sparse_adam: exp_avg must match its table")
-        want_v = (p.shape[0],) if rowwise else tuple(p.shape)
-        if tuple(v.shape) != want_v or not v.is_contiguous() or (rowwise and v.dtype != torch.float32):
+        if (v.shape != ((shape[0],) if rowwise else shape) or not v.is_contiguous()
+                or (rowwise and v.dtype != f32)):
             raise ValueError("[micro_engram] sparse_adam: exp_avg_sq has the wrong shape or dtype")
-        if r.dtype != torch.int64 or g.dtype != torch.float32 or g.shape != (r.numel(), dim):
+        k = r.numel()
+        if r.dtype != i64 or g.dtype != f32 or g.shape != (k, dim):
             raise ValueError("[micro_engram] sparse_adam: rows must be int64 [n], grads fp32 [n, D]")
-    rows = [r.contiguous() for r in rows]
-    grads = [g.contiguous() for g in grads]
+        if not r.is_contiguous():
+            r = r.contiguous()
+            held.append(r)
+        if not g.is_contiguous():
+            g = g.contiguous()
+            held.append(g)
+        pp.append(p.data_ptr())
+        mp.append(m.data_ptr())
+        vp.append(v.data_ptr())
+        rp.append(r.data_ptr())
+        gp.append(g.data_ptr())
+        counts.append(k)
     sq_code = dtype_code(exp_avg_sqs[0]) if not rowwise else ME_F32
-    call("me_sparse_adam", n, ptr_array([p.data_ptr() for p in params]),
-         ptr_array([m.data_ptr() for m in exp_avgs]), ptr_array([v.data_ptr() for v in exp_avg_sqs]),
-         ptr_array([r.data_ptr() for r in rows]), ptr_array([g.data_ptr() for g in grads]),
-         i64_array([r.numel() for r in rows]), i64_array([int(s) for s in steps]),
+    call("me_sparse_adam", n, ptr_array(pp), ptr_array(mp), ptr_array(vp), ptr_array(rp), ptr_array(gp),
+         i64_array(counts), i64_array([int(s) for s in steps]),
          i32_array([int(s) for s in stream_ids]), dim, dtype_code(params[0]), int(bool(rowwise)),
          sq_code, int(bool(lazy)), float(lr), float(betas[0]), float(betas[1]), float(eps),
          float(weight_decay), int(bool(stochastic_rounding)), int(seed) & ((1 << 64) - 1),

@@ -62,15 +62,24 @@ class LazyAdamW(torch.optim.Optimizer):
                 loss = closure()
         index = {id(p): i for i, p in enumerate(p for g in self.param_groups for p in g["params"])}
         for group in self.param_groups:
+            live = [p for p in group["params"]
+                    if p.grad is not None or getattr(p, "sparse_grad", None) is not None]
+            for p in live:
+                if not self.state[p]:
+                    self.init_state(self.state[p], p, group)
+            # every step counter in one call, and one host read for all of them (the
+            # counters are CPU tensors, as torch.optim.AdamW keeps them)
+            counters = [self.state[p]["step"] for p in live]
+            if counters:
+                torch._foreach_add_(counters, 1)
+                try:
+                    step_of = torch.stack(counters).tolist()
+                except RuntimeError:  # counters loaded onto different devices
+                    step_of = [float(c) for c in counters]
             batches = {}
-            for p in group["params"]:
+            for p, step in zip(live, step_of if counters else ()):
                 sparse = getattr(p, "sparse_grad", None)
-                if p.grad is None and sparse is None:
-                    continue
                 state = self.state[p]
-                if not state:
-                    self.init_state(state, p, group)
-                state["step"] += 1
                 n = p.shape[0] if p.dim() >= 1 else 1
                 rowwise = state["exp_avg_sq"].dim() == 1 and p.dim() >= 2
                 # the reference's lazy branches need rows (p.dim() >= 2); others are plain AdamW
@@ -78,9 +87,11 @@ class LazyAdamW(torch.optim.Optimizer):
                 if sparse is not None:
                     if not group["lazy"]:
                         raise ValueError("sparse row gradients need lazy=True")
-                    rows, g = sparse[0].long(), sparse[1].float()
+                    rows, g = sparse
+                    rows = rows if rows.dtype == torch.int64 else rows.long()
+                    g = g if g.dtype == torch.float32 else g.float()
                 else:
-                    g = p.grad.float()
+                    g = p.grad if p.grad.dtype == torch.float32 else p.grad.float()
                     rows = torch.arange(n, device=p.device)  # all-zero rows skip in the kernel
                 P = self._as_rows(p.data, n)
                 M = self._as_rows(state["exp_avg"], n)
@@ -94,7 +105,7 @@ class LazyAdamW(torch.optim.Optimizer):
                 b["exp_avg_sqs"].append(V)
                 b["rows"].append(rows)
                 b["grads"].append(g if g.dim() == 2 and g.shape[0] == rows.numel() else g.reshape(rows.numel(), -1))
-                b["steps"].append(int(state["step"].item()))
+                b["steps"].append(int(step))
                 b["stream_ids"].append(index[id(p)] % 65536)
             for (_, _, rowwise, lazy, _), b in batches.items():
                 ops.sparse_adam(b["params"], b["exp_avgs"], b["exp_avg_sqs"], b["rows"], b["grads"],

@@ -8,7 +8,9 @@ the radix-sort dedup kernel here (bit-exact: same unique keys, inverse and fp32 
 keep them per table as p.sparse_grad = (unique rows, fp32 sums) (rows.py:137-147). More than one
 rank needs that exchange, which this single-GPU build does not provide; it raises.
 """
+import contextlib
 import os
+import threading
 
 import torch
 
@@ -84,10 +86,63 @@ def _offsets_on(offsets, device):
     return t
 
 
+def _lookup_keys(idx2d, offs):
+    """Token-major keys of the lookups: lookup i*nt + k is (token i, table k), whose gradient
+    row is grad[i, k*D:(k+1)*D]; equal keys share a table, so within a key this is token order,
+    the order of the reference's table-major flattening. One launch: the sum is written
+    straight into the token-major buffer."""
+    nt, n = idx2d.shape
+    keys = torch.empty(n * nt, dtype=torch.int64, device=idx2d.device)
+    torch.add(idx2d.t(), offs, out=keys.view(n, nt))
+    return keys
+
+
+class _KeyPlan:
+    """The key half of a row lookup's dedup (unique keys, inverse, segment plan; torch.unique of
+    rows.py:81), made once: at the lookup, or when the launches issued after it are out
+    (key_plans_after)."""
+
+    def __init__(self, idx2d, offsets):
+        self.idx2d, self.offsets, self.outs = idx2d, offsets, None
+
+    def make(self):
+        if self.outs is None:
+            keys = _lookup_keys(self.idx2d, _offsets_on(self.offsets, self.idx2d.device)[:-1])
+            self.outs = ops.dedup_keys(keys, int(self.offsets[-1]))
+            self.idx2d = None
+        return self.outs
+
+
+_PLANS = threading.local()
+
+
+@contextlib.contextmanager
+def key_plans_after():
+    """Row lookups inside the block leave their key plans to the block's end, so that the host
+    issues them after the launches that follow the lookup (the gate): the training forward is
+    bound by the host's issue rate, and the plan's host work then overlaps the gate on the GPU.
+    On an exception the plans are left to the backward."""
+    outer = getattr(_PLANS, "pending", None)
+    _PLANS.pending = pending = []
+    try:
+        yield
+    finally:
+        _PLANS.pending = outer
+    for plan in pending:
+        plan.make()
+
+
 class _RowLookup(torch.autograd.Function):
     """Per-table rows for hashed ids, world size 1. Backward: the gradient rows of every lookup
     are deduplicated over (table, row) and added to each shard's sparse gradient (shards marked
-    _sparse_rows) or to a dense gradient (rows.py:71-134)."""
+    _sparse_rows) or to a dense gradient (rows.py:71-134).
+
+    The dedup's key half (unique keys, inverse and the segment plan; torch.unique of
+    rows.py:81) depends only on the row ids, so when a table needs its gradient the forward
+    makes it (after the gate's launches inside key_plans_after) and the backward runs only the
+    segment sums (rows.py:117-118). (On a second stream beside the gate it ran slower: a gate
+    tile holds a whole CU's LDS, so a dedup workgroup taking a CU between two rounds of gate
+    tiles delays the next round.)"""
 
     @staticmethod
     def forward(ctx, idx2d, offsets, *shards):
@@ -96,6 +151,14 @@ class _RowLookup(torch.autograd.Function):
         ctx.offsets = offsets
         ctx.shapes = [(s.shape, s.dtype) for s in shards]
         ctx.shards = shards if any(getattr(s, "_sparse_rows", False) for s in shards) else None
+        ctx.plan = None
+        if any(ctx.needs_input_grad[2:]) and idx2d.numel() > 0:
+            ctx.plan = _KeyPlan(idx2d, offsets)
+            pending = getattr(_PLANS, "pending", None)
+            if pending is None:
+                ctx.plan.make()
+            else:
+                pending.append(ctx.plan)
         return mem
 
     @staticmethod
@@ -105,15 +168,16 @@ class _RowLookup(torch.autograd.Function):
         D = ctx.shapes[0][0][1]
         offs_all = _offsets_on(ctx.offsets, idx2d.device)
         offs = offs_all[:-1]
-        # token-major flattening: lookup i*nt + k is (token i, table k), whose gradient row is
-        # grad[i, k*D:(k+1)*D]; equal keys share a table, so within a key this is token order,
-        # the order of the reference's table-major flattening
-        keys = (idx2d + offs[:, None]).t().reshape(-1)
+        if ctx.plan is not None:  # the key half ran in the forward
+            uniq_all, inv, count, plan = ctx.plan.make()
+            ctx.plan = None
+            outs = [uniq_all, inv, count, ops.dedup_sums(plan, count, grad.reshape(n * nt, D))]
+        else:
+            outs = ops.dedup(_lookup_keys(idx2d, offs), int(ctx.offsets[-1]), grad.reshape(n * nt, D))
         # one host read for the unique count and every table's bounds: keys past the count are
         # masked to the largest int64, so a search over the whole output stops at the count
-        outs = ops.dedup(keys, int(ctx.offsets[-1]), grad.reshape(n * nt, D))
         count = outs[2].reshape(1)
-        valid = torch.arange(outs[0].numel(), device=keys.device) < count
+        valid = torch.arange(outs[0].numel(), device=idx2d.device) < count
         masked = torch.where(valid, outs[0], torch.iinfo(torch.int64).max)
         host = torch.cat([count, torch.searchsorted(masked, offs_all)]).tolist()
         bounds = host[1:]
@@ -199,10 +263,13 @@ class RowTables:
             if sg is not None:
                 squares.append(sg[1])
                 scaled.append(sg[1])
-        for span in _spans(squares):
+        square_spans = _spans(squares)
+        for span in square_spans:
             ops.sumsq(span, sq, accumulate=True)
         if max_norm and max_norm > 0:
-            for span in _spans(scaled):
+            # the same tensors (fp32 gradients) make the same spans
+            same = len(squares) == len(scaled) and all(a is b for a, b in zip(squares, scaled))
+            for span in (square_spans if same else _spans(scaled)):
                 if span.is_contiguous() and span.data_ptr() % 16 == 0:
                     ops.clip_scale(span, sq, max_norm)
                 else:  # a view the kernel cannot scale in place: scale a copy, write it back

@@ -141,3 +141,21 @@ def test_identity_canon_tracking():
     assert not clone.identity_canon()
     eng.canon = torch.arange(50)
     assert eng.identity_canon()
+
+
+def test_gate_stats_fold_in_order_of_records():
+    # the recorded gates are reduced lazily (every 32 records and when read): the sums must be
+    # those of every record since the last read, over more records than one fold holds
+    eng = MicroEngram(model_dim=16, table_size=31, engram_dim=4, num_heads=1, orders=(2,), vocab_size=50)
+    gen = torch.Generator().manual_seed(5)
+    alphas = [torch.rand(17 + k, generator=gen) for k in range(75)]
+    alphas[3][0] = 0.995
+    for a in alphas:
+        eng._record_gate(a)
+    mean, sat = eng.pop_gate_stats()
+    allv = torch.cat(alphas).double()
+    assert mean == pytest.approx(float(allv.mean()), rel=1e-6)
+    assert sat == pytest.approx(float((allv > 0.99).double().mean()), rel=1e-6)
+    assert eng.pop_gate_stats() is None
+    eng._record_gate(torch.tensor([1.0, 0.0]))
+    assert eng.pop_gate_stats() == (0.5, 0.5)

@@ -343,6 +343,43 @@ def test_row_lookup_backward_sparse_grads():
         assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), acc.view(np.int32))
 
 
+def test_key_plan_after_gate_matches_plan_at_lookup():
+    # inject with gradients issues the dedup's key plan after the gate (key_plans_after); the
+    # same lookup outside that block makes it at once: same sparse gradients, bit for bit, and
+    # equal to the oracle's dedup of the ids with the memory gradient
+    eng = MicroEngram(model_dim=32, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3),
+                      vocab_size=500, seed=6).to(DEV)
+    shards = eng.shard_rows(0, 1, device=DEV)
+    for s in shards:
+        s._sparse_rows = True
+    ids = torch.randint(0, 500, (2, 48), device=DEV)
+    idx = eng.hash_ids(ids)
+    hidden = torch.randn(2, 48, 32, device=DEV)
+    gout = torch.randn(2, 48, 32, device=DEV)
+    got = []
+    for deferred in (True, False):
+        for s in shards:
+            s.sparse_grad = None
+        h = hidden.clone().requires_grad_(True)
+        if deferred:
+            out = eng.inject(h, idx)
+        else:
+            mem = eng._mem_grad(idx)
+            mem.retain_grad()
+            out = eng._gate(h, mem, None)
+        out.backward(gout)
+        got.append([(s.sparse_grad[0].clone(), s.sparse_grad[1].clone()) for s in shards])
+    for (ua, ga), (ub, gb) in zip(*got):
+        assert torch.equal(ua, ub)
+        assert torch.equal(ga.view(torch.int32), gb.view(torch.int32))
+    D = 8
+    for k, s in enumerate(shards):
+        g = mem.grad[:, k * D:(k + 1) * D].cpu().numpy()
+        u, _, acc = oracle.dedup(idx[k].reshape(-1).cpu().numpy(), g)
+        assert np.array_equal(got[1][k][0].cpu().numpy(), u)
+        assert np.array_equal(got[1][k][1].cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
 def _clip_engram(dtype, sparse):
     eng = MicroEngram(model_dim=16, table_size=64, engram_dim=8, num_heads=2, orders=(2,), vocab_size=50,
                       seed=4)
