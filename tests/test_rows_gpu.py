@@ -343,6 +343,27 @@ def test_row_lookup_backward_sparse_grads():
         assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), acc.view(np.int32))
 
 
+def test_row_lookup_retained_graph_second_backward():
+    # the first backward uses the forward's key plan, a second one over the retained graph runs
+    # the whole dedup again and merges into the sparse gradient (rows.py:125-129, 137-147)
+    eng = MicroEngram(model_dim=16, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3),
+                      vocab_size=500, seed=5)
+    shards = eng.shard_rows(0, 1, device=DEV)
+    for s in shards:
+        s._sparse_rows = True
+    ids = torch.randint(0, 500, (2, 40), device=DEV)
+    idx = eng.hash_ids(ids)
+    out = me_rows.row_lookup(eng, idx)
+    grads = [torch.randn_like(o) for o in out]
+    torch.autograd.backward(out, grads, retain_graph=True)
+    torch.autograd.backward(out, grads)
+    for k, s in enumerate(shards):
+        u1, _, a1 = oracle.dedup(idx[k].reshape(-1).cpu().numpy(), grads[k].reshape(-1, 8).cpu().numpy())
+        u, _, acc = oracle.dedup(np.concatenate([u1, u1]), np.concatenate([a1, a1]))
+        assert np.array_equal(s.sparse_grad[0].cpu().numpy(), u)
+        assert np.array_equal(s.sparse_grad[1].cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
 def test_key_plan_after_gate_matches_plan_at_lookup():
     # inject with gradients issues the dedup's key plan after the gate (key_plans_after); the
     # same lookup outside that block makes it at once: same sparse gradients, bit for bit, and
