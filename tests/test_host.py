@@ -159,3 +159,23 @@ def test_gate_stats_fold_in_order_of_records():
     assert eng.pop_gate_stats() is None
     eng._record_gate(torch.tensor([1.0, 0.0]))
     assert eng.pop_gate_stats() == (0.5, 0.5)
+
+
+def test_canon_in_state_dict_like_reference():
+    # the reference's test_canon.py:58-66: the map is in the state dict, an old checkpoint
+    # without it still loads (only canon missing), and the map round-trips; a loaded map also
+    # turns off the identity fast path (checked again after a load)
+    make = lambda canon=None: MicroEngram(model_dim=16, table_size=257, engram_dim=4, num_heads=2,
+                                          vocab_size=1000, canon=canon)
+    canon = torch.arange(1000)
+    canon[[5, 17, 600]] = 4
+    eng = make(canon)
+    assert "canon" in eng.state_dict()
+    old = {k: v for k, v in make().state_dict().items() if k != "canon"}
+    res = make().load_state_dict(old, strict=False)
+    assert list(res.missing_keys) == ["canon"] and not res.unexpected_keys
+    e2 = make()
+    assert e2.identity_canon()
+    e2.load_state_dict(eng.state_dict())
+    assert torch.equal(e2.canon, canon)
+    assert not e2.identity_canon()
