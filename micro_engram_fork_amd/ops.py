@@ -11,6 +11,7 @@ import functools
 from typing import List, Optional, Sequence
 
 import torch
+from torch._subclasses.fake_tensor import FakeTensor
 
 from . import _lib
 from ._lib import ME_BF16, ME_F32, ME_I32, ME_I64, ME_U8, call, i32_array, i64_array, ptr_array
@@ -51,6 +52,28 @@ def stream_of(device):
     return torch._C._cuda_getCurrentRawStream(index)
 
 
+def _custom_op(name):
+    """Registers the decorated function as the custom op micro_engram_amd::<name> (what
+    torch.compile traces and what a captured graph replays; its fake is added with
+    .register_fake) and returns a function that calls the implementation itself when nothing is
+    being traced: the op's dispatch costs ~20 us of host time per call, and an eager training
+    step is bound by the rate at which the host issues its launches. Under tracing, or for fake
+    tensors, calls go through the op."""
+    def wrap(fn):
+        op = torch.library.custom_op(f"micro_engram_amd::{name}", mutates_args=())(fn)
+
+        @functools.wraps(fn)
+        def dispatch(*args, **kwargs):
+            if torch.compiler.is_compiling() or (args and isinstance(args[0], FakeTensor)):
+                return op(*args, **kwargs)
+            return fn(*args, **kwargs)
+
+        dispatch.op = op
+        dispatch.register_fake = op.register_fake
+        return dispatch
+    return wrap
+
+
 def _p(t):
     return None if t is None else t.data_ptr()
 
@@ -88,7 +111,7 @@ def _table_args(table_orders, table_rows):
     return len(table_orders), i32_array(list(table_orders)), i64_array(list(table_rows))
 
 
-@torch.library.custom_op("micro_engram_amd::hash_ids", mutates_args=())
+@_custom_op("hash_ids")
 def hash_ids(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], canon: torch.Tensor,
              mults: torch.Tensor, table_orders: List[int], table_rows: List[int],
              pad_id: int, identity_canon: bool = False) -> torch.Tensor:
@@ -122,7 +145,7 @@ def _prev_ids(ids):
     return ids
 
 
-@torch.library.custom_op("micro_engram_amd::hash_prev", mutates_args=())
+@_custom_op("hash_prev")
 def hash_prev(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
               table_orders: List[int], table_rows: List[int], pad_id: int,
               identity_canon: bool = False) -> torch.Tensor:
@@ -155,7 +178,7 @@ def _tables_arg(tables: Sequence[torch.Tensor]):
     return ptr_array([t.data_ptr() for t in tables]), i64_array([t.shape[0] for t in tables]), dim
 
 
-@torch.library.custom_op("micro_engram_amd::gather", mutates_args=())
+@_custom_op("gather")
 def gather(idx: torch.Tensor, tables: List[torch.Tensor]) -> torch.Tensor:
     """mem [N, n_tables * D] from row ids int64 [n_tables, N] (module.py:146-154, 233; rows
     outside a table read as zeros, micro_engram_vllm/tp.py:20-39)."""
@@ -177,7 +200,7 @@ def _(idx, tables):
     return tables[0].new_empty((idx.shape[1], len(tables) * tables[0].shape[1]))
 
 
-@torch.library.custom_op("micro_engram_amd::hash_gather", mutates_args=())
+@_custom_op("hash_gather")
 def hash_gather(input_ids: torch.Tensor, position_ids: Optional[torch.Tensor], canon: torch.Tensor,
                 mults: torch.Tensor, table_orders: List[int], table_rows: List[int], pad_id: int,
                 tables: List[torch.Tensor], with_idx: bool,
@@ -209,7 +232,7 @@ def _(input_ids, position_ids, canon, mults, table_orders, table_rows, pad_id, t
     return [mem]
 
 
-@torch.library.custom_op("micro_engram_amd::hash_prev_gather", mutates_args=())
+@_custom_op("hash_prev_gather")
 def hash_prev_gather(ids: torch.Tensor, canon: torch.Tensor, mults: torch.Tensor,
                      table_orders: List[int], table_rows: List[int], pad_id: int,
                      tables: List[torch.Tensor], with_idx: bool,
@@ -282,7 +305,7 @@ def _gate_operands(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, ga
     return x, mem, w_key, w_value, q_scale_delta, k_scale_delta, scale_code, keep_u8, N, d, M
 
 
-@torch.library.custom_op("micro_engram_amd::gate_residual", mutates_args=())
+@_custom_op("gate_residual")
 def gate_residual(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
                   w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
                   k_scale_delta: Optional[torch.Tensor], gate_mode: int,
@@ -323,7 +346,7 @@ def _(hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_mode, keep
     return res
 
 
-@torch.library.custom_op("micro_engram_amd::kv_proj", mutates_args=())
+@_custom_op("kv_proj")
 def kv_proj(mem: torch.Tensor, w_key: torch.Tensor, w_value: torch.Tensor) -> torch.Tensor:
     """[K | V] [N, 2d] in mem's dtype: the key and value nn.Linear outputs of
     MicroEngram.inject (module.py:245, 254) for few tokens, in one hand-written MFMA kernel
@@ -349,7 +372,7 @@ def _(mem, w_key, w_value):
     return mem.new_empty((mem.shape[0], 2 * w_key.shape[0]))
 
 
-@torch.library.custom_op("micro_engram_amd::gate_residual_rows", mutates_args=())
+@_custom_op("gate_residual_rows")
 def gate_residual_rows(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
                        w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
                        k_scale_delta: Optional[torch.Tensor], gate_mode: int,
@@ -398,7 +421,7 @@ def gate_backward_workspace_bytes(n, d):
     return size.value
 
 
-@torch.library.custom_op("micro_engram_amd::gate_backward", mutates_args=())
+@_custom_op("gate_backward")
 def gate_backward(grad_out: torch.Tensor, hidden: torch.Tensor, mem: torch.Tensor,
                   w_key: torch.Tensor, w_value: torch.Tensor,
                   q_scale_delta: Optional[torch.Tensor], k_scale_delta: Optional[torch.Tensor],
@@ -456,7 +479,7 @@ def dedup_workspace_bytes(n):
     return size.value
 
 
-@torch.library.custom_op("micro_engram_amd::dedup", mutates_args=())
+@_custom_op("dedup")
 def dedup(keys: torch.Tensor, key_bound: int, grads: Optional[torch.Tensor]) -> List[torch.Tensor]:
     """[uniq [n], inv [n], count [1]] or [uniq, inv, count, gsum [n, D]]: torch.unique(keys,
     return_inverse=True) with the fp32 index_add_ sums of `grads` (micro_engram/rows.py:81,
@@ -602,11 +625,23 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
         gp.append(g.data_ptr())
         counts.append(k)
     sq_code = dtype_code(exp_avg_sqs[0]) if not rowwise else ME_F32
-    call("me_sparse_adam", n, ptr_array(pp), ptr_array(mp), ptr_array(vp), ptr_array(rp), ptr_array(gp),
-         i64_array(counts), i64_array([int(s) for s in steps]),
-         i32_array([int(s) for s in stream_ids]), dim, dtype_code(params[0]), int(bool(rowwise)),
-         sq_code, int(bool(lazy)), float(lr), float(betas[0]), float(betas[1]), float(eps),
-         float(weight_decay), int(bool(stochastic_rounding)), int(seed) & ((1 << 64) - 1),
+    sparse_adam_launch(dev, ptr_array(pp), ptr_array(mp), ptr_array(vp), n, dim, dtype_code(params[0]),
+                       sq_code, ptr_array(rp), ptr_array(gp), i64_array(counts), steps, stream_ids,
+                       lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, rowwise=rowwise, lazy=lazy,
+                       stochastic_rounding=stochastic_rounding, seed=seed)
+
+
+def sparse_adam_launch(dev, param_ptrs, exp_avg_ptrs, exp_avg_sq_ptrs, n, dim, dtype, sq_dtype,
+                       row_ptrs, grad_ptrs, counts, steps, stream_ids, *, lr, betas, eps, weight_decay,
+                       rowwise, lazy, stochastic_rounding, seed):
+    """The launch of sparse_adam from pointer arrays (ctypes) that a caller has already checked
+    against the tensors' shapes: n tables of [rows, dim] elements of `dtype`, their moments, and
+    for each its `counts[k]` unique int64 rows and fp32 [counts[k], dim] gradient rows. For callers
+    that keep the arrays of tensors which stay put between steps (the optimizer)."""
+    call("me_sparse_adam", n, param_ptrs, exp_avg_ptrs, exp_avg_sq_ptrs, row_ptrs, grad_ptrs, counts,
+         i64_array([int(s) for s in steps]), i32_array([int(s) for s in stream_ids]), dim, dtype,
+         int(bool(rowwise)), sq_dtype, int(bool(lazy)), float(lr), float(betas[0]), float(betas[1]),
+         float(eps), float(weight_decay), int(bool(stochastic_rounding)), int(seed) & ((1 << 64) - 1),
          stream_of(dev))
 
 

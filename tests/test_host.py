@@ -179,3 +179,29 @@ def test_canon_in_state_dict_like_reference():
     e2.load_state_dict(eng.state_dict())
     assert torch.equal(e2.canon, canon)
     assert not e2.identity_canon()
+
+
+def test_ops_route_fake_tensors_to_the_registered_ops():
+    # eager calls run the implementations directly; fake tensors (shape propagation, as under
+    # torch.compile) must reach the registered ops and their fake functions instead
+    from torch._subclasses.fake_tensor import FakeTensor, FakeTensorMode
+    from micro_engram_fork_amd import ops
+
+    assert hasattr(ops.gather, "op") and hasattr(ops.gate_residual_rows, "op")
+    with FakeTensorMode():
+        ids = torch.empty(32, 4, dtype=torch.int32, device="cuda")
+        canon = torch.empty(500, dtype=torch.int64, device="cuda")
+        mults = torch.empty(4, 3, dtype=torch.int64, device="cuda")
+        idx = ops.hash_prev(ids, canon, mults, [2, 2, 3, 3], [97, 97, 89, 89], 0, True)
+        assert isinstance(idx, FakeTensor) and tuple(idx.shape) == (4, 32)
+        tables = [torch.empty(97, 8, dtype=torch.bfloat16, device="cuda") for _ in range(4)]
+        mem = ops.gather(idx, tables)
+        assert isinstance(mem, FakeTensor) and tuple(mem.shape) == (32, 32)
+        hidden = torch.empty(32, 64, dtype=torch.bfloat16, device="cuda")
+        wk = torch.empty(64, 32, dtype=torch.bfloat16, device="cuda")
+        kv = ops.kv_proj(mem, wk, wk)
+        assert tuple(kv.shape) == (32, 128)
+        outs = ops.gate_residual_rows(hidden, mem, wk, wk, None, None, 0, None, True)
+        assert tuple(outs[0].shape) == (32, 64) and tuple(outs[1].shape) == (32,)
+        outs = ops.gate_residual(hidden, mem, wk, wk, None, None, 0, None, True)
+        assert isinstance(outs[0], FakeTensor) and tuple(outs[0].shape) == (32, 64)
