@@ -179,31 +179,33 @@ class _RowLookup(torch.autograd.Function):
         count = outs[2].reshape(1)
         valid = torch.arange(outs[0].numel(), device=idx2d.device) < count
         masked = torch.where(valid, outs[0], torch.iinfo(torch.int64).max)
+        # every unique key's row in its own table, in a few launches for all tables, queued
+        # before the host read (past the count the values are unused)
+        local_all = masked - offs[torch.searchsorted(offs, masked, right=True) - 1]
         host = torch.cat([count, torch.searchsorted(masked, offs_all)]).tolist()
-        bounds = host[1:]
-        uniq, gsum = outs[0][:host[0]], outs[3][:host[0]]
-        # every unique key's row in its own table, in a few launches for all tables
-        local_all = uniq - offs[torch.searchsorted(offs, uniq, right=True) - 1]
+        cnt, bounds = host[0], host[1:]
+        # each table's slice of the unique rows and sums (bounds[0] = 0, bounds[nt] = count)
+        sizes = [bounds[k + 1] - bounds[k] for k in range(nt)]
+        locals_ = local_all[:cnt].split(sizes)
+        sums = outs[3][:cnt].split(sizes)
         grads = []
         for k, (shape, dtype) in enumerate(ctx.shapes):
             if not ctx.needs_input_grad[2 + k]:
                 grads.append(None)
                 continue
-            a, b = bounds[k], bounds[k + 1]
-            local = local_all[a:b]
             if ctx.shards is not None and getattr(ctx.shards[k], "_sparse_rows", False):
                 shard = ctx.shards[k]
                 if getattr(shard, "sparse_grad", None) is None:
                     # this table's part of the dedup is already coalesced: unique rows in
                     # ascending order and fp32 sums that start from +0.0, as index_add_'s do
                     # (what add_sparse_grad would return for it, without a second dedup)
-                    shard.sparse_grad = (local, gsum[a:b])
+                    shard.sparse_grad = (locals_[k], sums[k])
                 else:
-                    add_sparse_grad(shard, local, gsum[a:b])
+                    add_sparse_grad(shard, locals_[k], sums[k])
                 grads.append(None)
                 continue
             g = torch.zeros(shape, dtype=torch.float32, device=grad.device)
-            g[local] = gsum[a:b]  # unique rows: a plain scatter
+            g[locals_[k]] = sums[k]  # unique rows: a plain scatter
             grads.append(g.to(dtype))
         return (None, None, *grads)
 
