@@ -302,11 +302,16 @@ extern "C" int me_kv_proj(const void *mem, int64_t n, int64_t mem_dim, const voi
     // 64 x 96 (a 256-token decode step's projection: 15.8-16.0 us against 17.8 us with 128 x 96
     // and a five-slot ring; 128 x 64, 64 x 128 and 32 x 96 there: 17-20 us) -- and larger batches
     // the 128 x 192 tile, which moves the fewest bytes per MFMA (512 tokens 26.8 us, 1024 tokens
-    // 50 us). fp32: 128 x 128 (MFMA-bound).
+    // 50 us). fp32 (model dim 1024, mem dim 1024): small tiles fill the CUs and two workgroups
+    // share one -- up to 768 tokens 32 x 64 (256 tokens 16.7 us against 72.5 with 128 x 128),
+    // up to 1024 32 x 128 (40.9 us), above 64 x 128 with a three-slot ring (2048 tokens 72.3 us
+    // against 74.8, 8192 tokens 276 against 295).
     if (dtype == ME_BF16) {
         if (n <= 64) return launch<uint16_t, 1, 3, 4>(a, s);
         if (n <= 256) return launch<uint16_t, 2, 3, 4>(a, s);
         return launch<uint16_t, 4, 6, 4>(a, s);
     }
-    return launch<float, 4, 4, 5>(a, s);
+    if (n <= 768) return launch<float, 1, 2, 5>(a, s);
+    if (n <= 1024) return launch<float, 1, 4, 4>(a, s);
+    return launch<float, 2, 4, 3>(a, s);
 }

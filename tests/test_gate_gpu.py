@@ -274,7 +274,8 @@ def test_rows_path_matches_fused_and_oracle(hdt, tdt, gate, n, d, m):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("n,d,m", [(1, 64, 32), (5, 24, 40), (128, 520, 96), (129, 256, 8),
-                                   (256, 5376, 1536), (300, 1024, 1024), (2048, 1024, 1024)])
+                                   (256, 5376, 1536), (300, 1024, 1024), (1000, 1024, 1024),
+                                   (2048, 1024, 1024)])
 def test_kv_proj_matches_fp32_reference(dtype, n, d, m):
     """me_kv_proj against torch's fp32 products of the same operands, rounded to the dtype:
     [K | V] = round(mem W_K^T | mem W_V^T). Tolerance: the sums run in another order, so after
