@@ -380,7 +380,7 @@ class MicroEngram(nn.Module):
     # of them idle below the last round. Measured on MI355X (model dim 5376, memory dim 1536,
     # bf16): 256 tokens 33 us against 73, 1024 tokens 61 against 74, 1536 tokens 88 against 76.
     # fp32 engrams: the fused kernel's fp32 tiles are 256 x 256 on 32x32x2 MFMAs, so a 2048-token
-    # batch (model dim 1024) gives it 32 tiles per pass (538 us) and the few-token path (83 us for
+    # batch (model dim 1024) gives it 32 tiles per pass (538 us) and the few-token path (72 us for
     # the projection) stays ahead far longer.
     few_tokens_max = 1024
     few_tokens_max_fp32 = 16384
