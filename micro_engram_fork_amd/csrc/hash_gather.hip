@@ -301,9 +301,16 @@ int fill_gather(LookupArgs &a, const void *const *tables, int32_t dim, int dtype
     return ME_OK;
 }
 
+// Workgroups a launch keeps when its tokens allow: fewer tokens per workgroup for small batches
+// (a 256-token decode step, the 2048-token fp32 case) so that every CU gets work.
+constexpr int64_t kMinBlocks = 512;
+
 template <int MODE>
-int launch(const LookupArgs &a, int vec, hipStream_t stream, const char *what) {
-    if (a.n == 0) return ME_OK;
+int launch(const LookupArgs &a0, int vec, hipStream_t stream, const char *what) {
+    if (a0.n == 0) return ME_OK;
+    LookupArgs a = a0;
+    while (a.tpb > 1 && ceil_div(a.n, static_cast<int64_t>(a.tpb)) < kMinBlocks) a.tpb >>= 1;
+    a.tpb_shift = log2_exact(a.tpb);
     const dim3 grid(static_cast<unsigned>(ceil_div(a.n, a.tpb)));
     if (a.mem == nullptr) {
         hipLaunchKernelGGL((lookup_kernel<MODE, 16, false>), grid, dim3(kBlock), 0, stream, a);
