@@ -56,7 +56,7 @@ class LazyAdamW(torch.optim.Optimizer):
 
     def _launch_plan(self, gi, group, live):
         """The parts of group gi's launches that stay put between steps, for the live parameters:
-        per (dtype, width, row-wise, lazy) batch the checked table / moment pointer arrays, the
+        per (device, dtype, width, row-wise, lazy) batch the checked table / moment pointer arrays, the
         members' positions in `live`, their noise stream ids and the tensors the kernel writes.
         Kept while every parameter keeps its storage and shape and its state the same tensors
         (load_state_dict, a new .data or new parameters make a new plan)."""
@@ -85,7 +85,7 @@ class LazyAdamW(torch.optim.Optimizer):
             if M.shape != P.shape or M.dtype != P.dtype or V.shape != ((n,) if rowwise else P.shape) or (
                     rowwise and V.dtype != torch.float32):
                 raise ValueError("[micro_engram] LazyAdamW: optimizer state does not match its parameter")
-            b = batches.setdefault((P.dtype, P.shape[1], rowwise, lazy, V.dtype),
+            b = batches.setdefault((P.device, P.dtype, P.shape[1], rowwise, lazy, V.dtype),
                                    {"pos": [], "P": [], "M": [], "V": [], "stream_ids": [], "written": [],
                                     "arange": []})
             b["pos"].append(i)
@@ -95,8 +95,8 @@ class LazyAdamW(torch.optim.Optimizer):
             b["stream_ids"].append(index[id(p)] % 65536)
             b["written"] += [p, state["exp_avg"], state["exp_avg_sq"]]
             b["arange"].append(None)  # all rows of a dense gradient, made on first use
-        for (dtype, dim, rowwise, lazy, vdtype), b in batches.items():
-            b.update(dim=dim, dtype=ops.dtype_code(torch.empty(0, dtype=dtype)), rowwise=rowwise, lazy=lazy,
+        for (device, dtype, dim, rowwise, lazy, vdtype), b in batches.items():
+            b.update(device=device, dim=dim, dtype=ops.dtype_code(torch.empty(0, dtype=dtype)), rowwise=rowwise, lazy=lazy,
                      sq_dtype=ops.ME_F32 if rowwise else ops.dtype_code(torch.empty(0, dtype=vdtype)),
                      P_arr=ops.ptr_array(b["P"]), M_arr=ops.ptr_array(b["M"]), V_arr=ops.ptr_array(b["V"]))
         plan = plans[gi] = {"key": key, "members": members, "batches": list(batches.values())}
@@ -158,7 +158,7 @@ class LazyAdamW(torch.optim.Optimizer):
                     gp.append(g.data_ptr())
                     counts.append(k)
                     steps.append(int(step_of[i]))
-                ops.sparse_adam_launch(live[b["pos"][0]].device, b["P_arr"], b["M_arr"], b["V_arr"], len(rp), dim,
+                ops.sparse_adam_launch(b["device"], b["P_arr"], b["M_arr"], b["V_arr"], len(rp), dim,
                                        b["dtype"], b["sq_dtype"], ops.ptr_array(rp), ops.ptr_array(gp),
                                        ops.i64_array(counts), steps, b["stream_ids"], lr=group["lr"],
                                        betas=group["betas"], eps=group["eps"],
