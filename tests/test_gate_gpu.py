@@ -22,7 +22,8 @@ DEV = "cuda"
 @pytest.fixture(autouse=True, params=["fused", "rows"])
 def gate_path(request, monkeypatch):
     """Every test of this file runs on both gate paths of MicroEngram: the fused two-pass kernel
-    (me_gate_residual) and, for few tokens, the library GEMM + row kernel (me_gate_rows)."""
+    (me_gate_residual) and, for few tokens, the hand-written projection (me_kv_proj) + row
+    kernel (me_gate_rows)."""
     limit = 0 if request.param == "fused" else 1 << 30
     monkeypatch.setattr(MicroEngram, "few_tokens_max", limit)
     monkeypatch.setattr(MicroEngram, "few_tokens_max_fp32", limit)
@@ -202,19 +203,19 @@ def test_tiny_forward_fp32_full():
     assert_close_out(out, ref.reshape(out.shape), hidden, torch.float32)
 
 
-def test_gemma_prefill_forward_sampled():
+def test_gemma_prefill_forward_full():
+    # the headline workload end to end: all 8192 tokens of a Gemma-scale prefill batch (fused
+    # hash + gather, then the 256 x 224 gate passes) against the oracle's inject on the same rows
     eng = synthetic.build_engram("gemma", DEV, seed=0).eval()
     ids, pos, hidden = synthetic.prefill_inputs(seed=0, device=DEV)
     with torch.no_grad():
         out = eng(hidden, ids, pos)
         idx = torch.stack(eng.hash_ids(ids, pos)).reshape(len(eng.tables), -1)
-    sample = torch.from_numpy(np.random.Generator(np.random.PCG64(1)).choice(8192, 256, replace=False)).to(DEV)
-    mem = torch.cat([t.weight[idx[k][sample]] for k, t in enumerate(eng.tables)], dim=-1).cpu()
-    h = hidden.reshape(-1, hidden.shape[-1])[sample].cpu()
+        mem = torch.cat([t.weight[idx[k]] for k, t in enumerate(eng.tables)], dim=-1).cpu()
+    h = hidden.reshape(-1, hidden.shape[-1]).cpu()
     ref = oracle.inject(h, mem, eng.key.weight.detach().cpu(), eng.value.weight.detach().cpu(),
                         "scalar_sqrt", eng.q_scale.detach().cpu(), eng.k_scale.detach().cpu())
-    got = out.reshape(-1, out.shape[-1])[sample]
-    assert_close_out(got, ref, h, torch.bfloat16)
+    assert_close_out(out.reshape(-1, out.shape[-1]), ref, h, torch.bfloat16)
     del eng
     torch.cuda.empty_cache()
 
@@ -303,7 +304,7 @@ def test_kv_proj_matches_fp32_reference(dtype, n, d, m):
         assert bool(((got.double() - exact).abs() <= 2e-6 * scale + 1e-30).all())
 
 
-def test_serving_decode_step_sampled():
+def test_serving_decode_step_full():
     # the serving decode workload: 256 sequences x 1 token (0-3 history tokens, -1 = none) on the
     # Gemma-scale tables, hash_prev + inject as the vLLM layer calls them, against the oracle
     eng = synthetic.build_engram("gemma", DEV, seed=0).eval()
