@@ -176,3 +176,42 @@ def test_sparse_row_gradients_equal_dense():
         assert torch.equal(sums, want[rows])
     assert torch.equal(dense.key.weight.grad, sparse.key.weight.grad)
     rt.zero_grad()
+
+
+def test_backward_gemma_prefill_full():
+    # the training step's backward at the headline shape: 8192 tokens, model dim 5376, 24 bf16
+    # tables of the Gemma-scale sizes (dense table gradients here; the sparse row path is
+    # checked against these by test_sparse_row_gradients_equal_dense), every gradient against
+    # torch autograd of the oracle on the CPU
+    eng = synthetic.build_engram("gemma", DEV, seed=7).train()
+    ids, pos, hidden = synthetic.prefill_inputs(seed=5, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    grad_out = torch.randn(hidden.shape, generator=gen, device=DEV).to(torch.bfloat16)
+    idx = eng.hash_ids(ids, pos)
+    d = hidden.shape[-1]
+    # tokens whose score is near 0 get no output gradient (see _conditioned)
+    mem = torch.cat([t.weight.detach()[i.reshape(-1)] for i, t in zip(idx, eng.tables)], -1).cpu()
+    _, alpha = oracle.inject(hidden.cpu().reshape(-1, d), mem, eng.key.weight.detach().cpu(),
+                             eng.value.weight.detach().cpu(), eng.gate, eng.q_scale.detach().cpu(),
+                             eng.k_scale.detach().cpu(), return_alpha=True)
+    ok = (torch.log(alpha / (1 - alpha)).abs() >= 0.1).to(grad_out.dtype).to(DEV)
+    grad_out = grad_out * ok.reshape(*grad_out.shape[:-1], 1)
+
+    eng.zero_grad(set_to_none=True)
+    h = hidden.detach().clone().requires_grad_(True)
+    eng.inject(h, idx).backward(grad_out)
+    got = {"hidden": h.grad, "key": eng.key.weight.grad, "value": eng.value.weight.grad,
+           "q_scale": eng.q_scale.grad, "k_scale": eng.k_scale.grad}
+    got.update({f"table{k}": t.weight.grad for k, t in enumerate(eng.tables)})
+
+    leaf = lambda t: t.detach().cpu().clone().requires_grad_(True)
+    tables = [leaf(t.weight) for t in eng.tables]
+    wk, wv, dq, dk, hc = leaf(eng.key.weight), leaf(eng.value.weight), leaf(eng.q_scale), leaf(eng.k_scale), leaf(hidden)
+    mem = torch.cat([F.embedding(i.cpu().reshape(-1), t) for i, t in zip(idx, tables)], dim=-1)
+    out = oracle.inject(hc.reshape(-1, d), mem, wk, wv, eng.gate, dq, dk)
+    out.backward(grad_out.cpu().reshape(-1, d).to(out.dtype))
+    want = {"hidden": hc.grad, "key": wk.grad, "value": wv.grad, "q_scale": dq.grad, "k_scale": dk.grad}
+    want.update({f"table{k}": t.grad for k, t in enumerate(tables)})
+    _assert_grads_close(got, want, torch.bfloat16)
+    del eng, got, want
+    torch.cuda.empty_cache()
