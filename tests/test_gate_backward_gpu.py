@@ -213,5 +213,24 @@ def test_backward_gemma_prefill_full():
     want = {"hidden": hc.grad, "key": wk.grad, "value": wv.grad, "q_scale": dq.grad, "k_scale": dk.grad}
     want.update({f"table{k}": t.grad for k, t in enumerate(tables)})
     _assert_grads_close(got, want, torch.bfloat16)
-    del eng, got, want
+    del want, tables, mem, out, hc
+
+    # the same batch through row shards with sparse gradients (the key plan made in the forward,
+    # the segment sums in the backward): each table's (rows, fp32 sums) are its dense gradient's
+    # non-zero rows, and the other gradients are the dense path's, bit for bit
+    key_grad, hidden_grad = got["key"].clone(), got["hidden"].clone()
+    eng.zero_grad(set_to_none=True)
+    shards = eng.shard_rows(0, 1, device=DEV)
+    rt = RowTables([("e", eng)], lazy=True, rowwise=True, sparse_grads=True)
+    h2 = hidden.detach().clone().requires_grad_(True)
+    eng.inject(h2, idx).backward(grad_out)
+    for k, shard in enumerate(shards):
+        rows, sums = shard.sparse_grad
+        dense = got[f"table{k}"]
+        assert torch.equal(sums.to(dense.dtype), dense[rows])
+        assert bool(torch.isin(dense.abs().sum(-1).nonzero().reshape(-1), rows).all())
+    assert torch.equal(eng.key.weight.grad, key_grad)
+    assert torch.equal(h2.grad, hidden_grad)
+    rt.zero_grad()
+    del eng, got, shards
     torch.cuda.empty_cache()
