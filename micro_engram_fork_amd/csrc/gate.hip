@@ -759,12 +759,16 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     // with them the key pass loads its scale deltas and the value pass the key pass's partial
     // sums of token n0 + tid (kPartLoads column tiles, always that many loads so that the slab
     // waits count a fixed number; the ones past n_jt read zeros and are not summed)
-    constexpr int kPfRows = PHASE == kKey ? 16 : 8;
+    // The backward's passes (kGradValue: V and the output gradient g; kGradKey: K, hidden and g)
+    // load nothing under their slabs; their per-token values (the gate with keep folded in, or
+    // the three coefficients) are read before the K loop and used after it.
+    constexpr int kPfRows = PHASE == kKey ? 16 : (PHASE == kValue ? 8 : 0);
     constexpr int kPartLoads = 24;
-    constexpr int kPfLoads = kPfRows + (PHASE == kKey ? 4 : kPartLoads);
+    constexpr int kPfLoads = PHASE == kKey ? kPfRows + 4 : (PHASE == kValue ? kPfRows + kPartLoads : 0);
     const int64_t n_tok = n0 + tid;
     const bool parts_late = PHASE == kValue && a.n_jt <= kPartLoads;
     float alpha_reg = 0.f;
+    float coef_reg[3] = {0.f, 0.f, 0.f};
     // the gate of token n_tok, summed in column tile order exactly as gate_alpha_kernel sums
     // them (the tiles of column tile 0 also write the gates and row stats the caller asked for)
     auto set_alpha = [&](float sk2, float sck, float sx2) {
@@ -784,7 +788,7 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     };
     u32x3_v part[PHASE == kValue ? kPartLoads : 1];
     u32x4_v xpre[32];
-    u32x4_v spre[PHASE == kKey ? 4 : 1];
+    u32x4_v spre[PHASE == kKey || PHASE == kGradKey ? 4 : 1];
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(a.hidden), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
     // byte offset of the lane's 16 bytes in its row u (token ntok0 + 4u + rsub) of hidden and of
@@ -803,20 +807,25 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
         for (int u = u0; u < u1; ++u)
             xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, row_off(u), 0, 0));
     };
+    // the scale deltas of the lane's 8 columns (key pass, grad-key pass)
+    auto load_scales = [&]() {
+        const int esz = a.scale_bf16 ? 2 : 4;
+        const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
+        spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+        spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
+        spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+    };
     auto prefetch = [&]() {
-        load_rows(0, kPfRows);
         if constexpr (PHASE == kKey) {
-            const int esz = a.scale_bf16 ? 2 : 4;
-            const uint32_t off = jok ? static_cast<uint32_t>(jl * esz) : a.scale_bytes;
-            const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<void *>(a.q_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
-            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<void *>(a.k_delta), 0, static_cast<int>(a.scale_bytes), kBufferConfig);
-            spre[0] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
-            spre[1] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rq, off + 16, 0, 0));
-            spre[2] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-            spre[3] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
-        } else {
+            load_rows(0, kPfRows);
+            load_scales();
+        } else if constexpr (PHASE == kValue) {
+            load_rows(0, kPfRows);
             // the partials are [n_jt][n][3] floats (n * d < 2^30 here, so under 2^31 bytes)
             const uint32_t pbytes = static_cast<uint32_t>(a.n_jt * a.n * 12);
             const __amdgpu_buffer_rsrc_t rp =
@@ -888,6 +897,16 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
         for (int i = 0; i < kDmaA; ++i) issue_a(sl, i);
 #pragma unroll
         for (int i = 0; i < kDmaB; ++i) issue_b(sl, i);
+    }
+    // the backward's per-token values, loaded while the first slabs land (issued after their
+    // row loads, so the first slab wait does not wait for them)
+    if (PHASE == kGradValue && n_tok < a.n) {
+        alpha_reg = a.row_stats[n_tok * 4 + 3];
+        if (a.keep != nullptr && a.keep[n_tok] == 0) alpha_reg = 0.f;
+    }
+    if (PHASE == kGradKey && n_tok < a.n) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) coef_reg[c] = a.tok_coef[n_tok * 3 + c];
     }
     // value pass, more than kPartLoads column tiles: the gate of token n0 + tid from the key
     // pass's partial sums while the first slabs land (otherwise the sums are loaded with the
@@ -987,7 +1006,23 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     for (int sl = pf_at + 2; sl < slabs; ++sl) slab(sl, NoWait{}, NoDma{});
     wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
     __syncthreads();  // the ring is free for the epilogue
-    load_rows(kPfRows, 32);
+    // operands of the backward's epilogues: the output gradient g (read) and the gradients
+    // written, all [n, d] bf16 like hidden (same byte offsets)
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.grad_out), 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+    const __amdgpu_buffer_rsrc_t rgp =
+        __builtin_amdgcn_make_buffer_rsrc(a.grad_proj, 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+    const __amdgpu_buffer_rsrc_t rgh =
+        __builtin_amdgcn_make_buffer_rsrc(a.grad_hidden, 0, static_cast<int>(a.hidden_bytes), kBufferConfig);
+    if constexpr (PHASE == kKey || PHASE == kValue) {
+        load_rows(kPfRows, 32);
+    } else if constexpr (PHASE == kGradValue) {
+#pragma unroll
+        for (int u = 0; u < 32; ++u)
+            xpre[u] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rg, row_off(u), 0, 0));
+    } else {
+        if (a.q_delta != nullptr) load_scales();
+    }
     if (parts_late && n_tok < a.n) {
         float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
 #pragma unroll
@@ -1002,11 +1037,16 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
 
     // ---- epilogue: each wave stages round_T of its 128 x 112 tile as [token][column] rows
     uint8_t *stage = ring + wave * kWaveStage16;
-    float *s_aux = reinterpret_cast<float *>(ring + 4 * kWaveStage16);  // key [2][256][3]; value [256]
-    if (PHASE == kValue) {
+    // s_aux: key [2 wj][256 tokens][3] sums; value [256] gates; grad value [256] gates, then
+    // [2 wj][256] sums of g . V; grad key [256][3] coefficients, then [2 wn][224 columns]
+    float *s_aux = reinterpret_cast<float *>(ring + 4 * kWaveStage16);
+    if (PHASE == kValue || PHASE == kGradValue) {
         s_aux[tid] = alpha_reg;
-    } else {
+    } else if (PHASE == kKey) {
         for (int e = tid; e < 2 * kTile * 3; e += kThreads) s_aux[e] = 0.f;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) s_aux[tid * 3 + c] = coef_reg[c];
     }
     // acc[x][y][e] is column 16x + 4 (lane >> 4) + e of token 16y + (lane & 15)
     {
@@ -1026,10 +1066,10 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
     }
     __syncthreads();  // staging (and s_aux) visible
 
-    float wcol[kLaneCols];  // q_scale * k_scale of the lane's columns (key pass)
+    float wcol[kLaneCols];  // q_scale * k_scale of the lane's columns (key and grad-key passes)
 #pragma unroll
     for (int e = 0; e < kLaneCols; ++e) wcol[e] = 1.f;
-    if (PHASE == kKey && jok && a.q_delta != nullptr) {
+    if ((PHASE == kKey || PHASE == kGradKey) && jok && a.q_delta != nullptr) {
         const uint32_t *qw = reinterpret_cast<const uint32_t *>(&spre[0]);
         const uint32_t *kw = reinterpret_cast<const uint32_t *>(&spre[2]);
 #pragma unroll
@@ -1045,52 +1085,133 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
             wcol[e] = (1.f + qv) * (1.f + kv);
         }
     }
-#pragma unroll
-    for (int u = 0; u < 32; ++u) {
-        const int row = u * 4 + rsub;
-        uint32_t cw[4] = {0u, 0u, 0u, 0u};
-        // lanes 14 and 15 of a row hold no columns: in the value pass they read the pad and the
-        // next row (or the gates past the last row; all inside the ring) and store nothing
+    // the staged row of the lane's 8 columns; lanes 14 and 15 of a row hold no columns: in the
+    // value pass they read the pad and the next row (or the gates past the last row; all inside
+    // the ring) and store nothing, elsewhere they take zeros so that row sums ignore them
+    auto staged = [&](int row, uint32_t (&cw)[4]) {
+        cw[0] = cw[1] = cw[2] = cw[3] = 0u;
         if (PHASE == kValue || l16 < kWJ / kLaneCols) {
             const uint8_t *sp = stage + row * kPitch16 + l16 * 16;
             const uint2 c0 = reinterpret_cast<const uint2 *>(sp)[0];
             const uint2 c1 = reinterpret_cast<const uint2 *>(sp)[1];
             cw[0] = c0.x; cw[1] = c0.y; cw[2] = c1.x; cw[3] = c1.y;
         }
-        const T *cv = reinterpret_cast<const T *>(cw);
-        const u32x4_v xq = xpre[u];
-        uint32_t xw[4] = {xq[0], xq[1], xq[2], xq[3]};
-        const H *xv = reinterpret_cast<const H *>(xw);
-        if constexpr (PHASE == kKey) {
-            float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
+    };
+    if constexpr (PHASE != kGradKey) {
 #pragma unroll
-            for (int e = 0; e < kLaneCols; ++e) {
-                const float kv = to_f<T>(cv[e]);
-                const float x = to_f<H>(xv[e]);
-                sk2 += kv * kv;
-                sck += x * wcol[e] * kv;
-                sx2 += x * x;
-            }
-            sk2 = row16_sum(sk2);
-            sck = row16_sum(sck);
-            sx2 = row16_sum(sx2);
-            if (l16 == 15) {
-                float *p = s_aux + (wj * kTile + wn * 128 + row) * 3;
-                p[0] = sk2;
-                p[1] = sck;
-                p[2] = sx2;
-            }
-        } else {
-            // x + round(alpha * V), V already rounded, two columns per conversion; a row past n
-            // or a lane past d stores nothing (its offset is the range end)
-            const float alpha = s_aux[wn * 128 + row];
-            u32x4_v o;
+        for (int u = 0; u < 32; ++u) {
+            const int row = u * 4 + rsub;
+            uint32_t cw[4];
+            staged(row, cw);
+            const T *cv = reinterpret_cast<const T *>(cw);
+            const u32x4_v xq = xpre[u];
+            uint32_t xw[4] = {xq[0], xq[1], xq[2], xq[3]};
+            const H *xv = reinterpret_cast<const H *>(xw);
+            if constexpr (PHASE == kKey) {
+                float sk2 = 0.f, sck = 0.f, sx2 = 0.f;
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const uint32_t av = pack_bf16(alpha * bf16_lo(cw[h]), alpha * bf16_hi(cw[h]));
-                o[h] = pack_bf16(bf16_lo(xw[h]) + bf16_lo(av), bf16_hi(xw[h]) + bf16_hi(av));
+                for (int e = 0; e < kLaneCols; ++e) {
+                    const float kv = to_f<T>(cv[e]);
+                    const float x = to_f<H>(xv[e]);
+                    sk2 += kv * kv;
+                    sck += x * wcol[e] * kv;
+                    sx2 += x * x;
+                }
+                sk2 = row16_sum(sk2);
+                sck = row16_sum(sck);
+                sx2 = row16_sum(sx2);
+                if (l16 == 15) {
+                    float *p = s_aux + (wj * kTile + wn * 128 + row) * 3;
+                    p[0] = sk2;
+                    p[1] = sck;
+                    p[2] = sx2;
+                }
+            } else if constexpr (PHASE == kValue) {
+                // x + round(alpha * V), V already rounded, two columns per conversion; a row past
+                // n or a lane past d stores nothing (its offset is the range end)
+                const float alpha = s_aux[wn * 128 + row];
+                u32x4_v o;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t av = pack_bf16(alpha * bf16_lo(cw[h]), alpha * bf16_hi(cw[h]));
+                    o[h] = pack_bf16(bf16_lo(xw[h]) + bf16_lo(av), bf16_hi(xw[h]) + bf16_hi(av));
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(o, ro, row_off(u), 0, kStoreNT);
+            } else {
+                // grad value: d alpha gets sum_j g_j V_j (keep is applied per token later);
+                // dV = alpha g, rounded to the engram dtype as the cast after the projection
+                // rounds it (xw holds g here)
+                const float alpha = s_aux[wn * 128 + row];
+                float gv = 0.f;
+                u32x4_v dv;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const float g0 = bf16_lo(xw[h]), g1 = bf16_hi(xw[h]);
+                    gv += g0 * bf16_lo(cw[h]);
+                    gv += g1 * bf16_hi(cw[h]);
+                    dv[h] = pack_bf16(alpha * g0, alpha * g1);
+                }
+                gv = row16_sum(gv);
+                if (l16 == 15) s_aux[kTile + wj * kTile + wn * 128 + row] = gv;
+                __builtin_amdgcn_raw_buffer_store_b128(dv, rgp, row_off(u), 0, kStoreNT);
             }
-            __builtin_amdgcn_raw_buffer_store_b128(o, ro, row_off(u), 0, kStoreNT);
+        }
+    } else {
+        // grad key, with the token's coefficients (ca, c2, c3) and w = q_scale k_scale:
+        //   d hidden = g + round(ca w K - c2 x), dK = ca w x - c3 K, scales: sum of ca x K;
+        // hidden and g rows are loaded eight rows at a time
+        float colp[kLaneCols];
+#pragma unroll
+        for (int e = 0; e < kLaneCols; ++e) colp[e] = 0.f;
+        constexpr int kGkBatch = 8;
+        for (int b0 = 0; b0 < 32; b0 += kGkBatch) {
+            u32x4_v xb[kGkBatch], gb[kGkBatch];
+#pragma unroll
+            for (int v = 0; v < kGkBatch; ++v) {
+                xb[v] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rh, row_off(b0 + v), 0, 0));
+                gb[v] = __builtin_bit_cast(u32x4_v, __builtin_amdgcn_raw_buffer_load_b128(rg, row_off(b0 + v), 0, 0));
+            }
+#pragma unroll
+            for (int v = 0; v < kGkBatch; ++v) {
+                const int u = b0 + v;
+                const int row = u * 4 + rsub;
+                uint32_t cw[4];
+                staged(row, cw);
+                const float *cf = s_aux + (wn * 128 + row) * 3;
+                const float ca = cf[0], c2 = cf[1], c3 = cf[2];
+                u32x4_v hv, kv;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    float K[2] = {bf16_lo(cw[h]), bf16_hi(cw[h])};
+                    float x[2] = {bf16_lo(xb[v][h]), bf16_hi(xb[v][h])};
+                    float g[2] = {bf16_lo(gb[v][h]), bf16_hi(gb[v][h])};
+                    float dh[2], dk[2];
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const float w = wcol[2 * h + q];
+                        const float dx = ca * w * K[q] - c2 * x[q];
+                        dh[q] = g[q] + round_t<H>(dx);
+                        dk[q] = ca * w * x[q] - c3 * K[q];
+                        colp[2 * h + q] += ca * x[q] * K[q];
+                    }
+                    hv[h] = pack_bf16(dh[0], dh[1]);
+                    kv[h] = pack_bf16(dk[0], dk[1]);
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(hv, rgh, row_off(u), 0, kStoreNT);
+                __builtin_amdgcn_raw_buffer_store_b128(kv, rgp, row_off(u), 0, kStoreNT);
+            }
+        }
+        // column sums over the wave's 128 tokens: the four row groups of a column are lanes
+        // l16, l16 + 16, l16 + 32, l16 + 48
+#pragma unroll
+        for (int e = 0; e < kLaneCols; ++e) {
+            colp[e] += __shfl_xor(colp[e], 16, 64);
+            colp[e] += __shfl_xor(colp[e], 32, 64);
+        }
+        if (rsub == 0 && l16 < kWJ / kLaneCols) {
+            float *pc = s_aux + 3 * kTile + wn * kTJ + wj * kWJ + l16 * kLaneCols;
+#pragma unroll
+            for (int e = 0; e < kLaneCols; ++e) pc[e] = colp[e];
         }
     }
     if constexpr (PHASE == kKey) {
@@ -1104,6 +1225,17 @@ __global__ __launch_bounds__(kThreads, 1) void gate224_kernel(const GateArgs a) 
             o[1] = p0[1] + p1[1];
             o[2] = p0[2] + p1[2];
         }
+    } else if constexpr (PHASE == kGradValue) {
+        __syncthreads();  // s_aux complete
+        const int64_t n = n0 + tid;
+        if (n < a.n)
+            a.grad_partials[static_cast<int64_t>(jt) * a.n + n] = s_aux[kTile + tid] + s_aux[2 * kTile + tid];
+    } else if constexpr (PHASE == kGradKey) {
+        __syncthreads();  // s_aux complete
+        const int64_t j = j0 + tid;
+        if (tid < kTJ && j < a.d)
+            a.col_partials[static_cast<int64_t>(nt) * a.d + j] =
+                s_aux[3 * kTile + tid] + s_aux[3 * kTile + kTJ + tid];
     }
 }
 
@@ -1204,8 +1336,8 @@ GradLayout grad_layout(int64_t n, int64_t d) {
     auto up = [](size_t x) { return (x + 255) & ~size_t{255}; };
     GradLayout l{};
     size_t off = 0;
-    l.partials = off;
-    off += up(static_cast<size_t>(ceil_div(d, kTile)) * static_cast<size_t>(n) * 4);
+    l.partials = off;  // per column tile: 224-column tiles make the most of them
+    off += up(static_cast<size_t>(ceil_div(d, kTJ)) * static_cast<size_t>(n) * 4);
     l.coef = off;
     off += up(static_cast<size_t>(n) * 3 * 4);
     l.cols = off;
@@ -1474,6 +1606,36 @@ extern "C" int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n,
     hipStream_t s = as_stream(stream);
     // value side (W_V, writes dV and the per-token sums of g . V), the per-token coefficients,
     // key side (W_K, writes d hidden and dK), then the scale gradients
+    const int64_t hidden_bytes = n * model_dim * static_cast<int64_t>(dtype_size(hidden_dtype));
+    if (dtype == ME_BF16 && hidden_dtype == ME_BF16 && hidden_bytes < (int64_t{1} << 31) &&
+        (mem_dim * 2) % kSlab == 0 && mem_dim * 2 >= 3 * kSlab) {
+        // bf16: the forward's 256 x 224 tiles (16x16x32 MFMAs, whole slabs, at least three)
+        a.hidden_bytes = static_cast<uint32_t>(hidden_bytes);
+        a.n_jt = static_cast<int>(ceil_div(model_dim, kTJ));
+        a.total_tiles = a.n_jt * a.n_nt;
+        a.per_xcd = static_cast<int>(ceil_div(a.total_tiles, kXcds));
+        GateArgs av = a, ak = a;
+        av.w = static_cast<const uint8_t *>(w_value);
+        av.grad_proj = static_cast<uint8_t *>(grad_value);
+        ak.w = static_cast<const uint8_t *>(w_key);
+        ak.grad_proj = static_cast<uint8_t *>(grad_key);
+        const dim3 grid16(static_cast<unsigned>(a.per_xcd * kXcds));
+        hipLaunchKernelGGL(gate224_kernel<kGradValue>, grid16, dim3(kThreads), 0, s, av);
+        int st_ = check_launch("me_gate_backward (value side)");
+        if (st_ != ME_OK) return st_;
+        hipLaunchKernelGGL(gate_grad_token_kernel, dim3(static_cast<unsigned>(ceil_div(n, kThreads))),
+                           dim3(kThreads), 0, s, a);
+        st_ = check_launch("me_gate_backward (token coefficients)");
+        if (st_ != ME_OK) return st_;
+        hipLaunchKernelGGL(gate224_kernel<kGradKey>, grid16, dim3(kThreads), 0, s, ak);
+        st_ = check_launch("me_gate_backward (key side)");
+        if (st_ != ME_OK) return st_;
+        if (gate_mode != ME_GATE_SCALAR_SQRT) return ME_OK;
+        hipLaunchKernelGGL(gate_grad_scale_kernel,
+                           dim3(static_cast<unsigned>(ceil_div(model_dim, kThreads))), dim3(kThreads), 0, s,
+                           a, grad_q_scale, grad_k_scale);
+        return check_launch("me_gate_backward (scale gradients)");
+    }
     GateArgs av = a, ak = a;
     av.w = static_cast<const uint8_t *>(w_value);
     av.grad_proj = static_cast<uint8_t *>(grad_value);
