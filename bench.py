@@ -581,8 +581,8 @@ def main():
         "roofline_update": {
             "kernel": "sparse update after the backward: segment sums of the gradient rows + "
                       "row-wise Adam with stochastic rounding (the key plan -- unique keys, "
-                      "inverse, segment bounds -- runs in the forward on a second stream, "
-                      "beside the gate; its time is key_plan_ms)",
+                      "inverse, segment bounds -- runs in the training forward, after the "
+                      "gate's launches on the same stream; its time is key_plan_ms)",
             "bound": "hbm",
             "achieved": update_gbs,
             "peak": HBM_PEAK_GBS,
