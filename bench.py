@@ -76,20 +76,21 @@ def parse():
     return ap.parse_args()
 
 
-# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,104.5
-# KiB per dispatch, x2.0) and WRITE_SIZE (24,586.4 KiB, x1.0), the factors being what the two
-# counters read for this script's 1 GiB device copy. A counter run cannot share a process with
-# the timing, so the figure is a measured constant, re-measured when the kernel changes.
-GATHER_TRAFFIC_BYTES = 49_966_464
+# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,433.5
+# KiB per dispatch, x2.0) and WRITE_SIZE (24,588.0 KiB, x1.0), the factors being what the two
+# counters read for this script's device copy of the gather's output size. A counter run cannot
+# share a process with the timing, so the figure is a measured constant, re-measured when the
+# kernel or its inputs change (the canon map's lines are in it).
+GATHER_TRAFFIC_BYTES = 50_641_920
 CYCLE = 16  # distinct prefill batches the timed steps cycle through
 
 
-def gather_bytes_per_token(eng, esize, canon_read):
+def gather_bytes_per_token(eng, esize):
     """Algorithmic bytes of the fused hash + gather per token: every table row read and written
-    once, plus the token id and its position, and one canon entry when the map is not the
-    identity (8 bytes each)."""
+    once, plus the token id, its position and its canon entry (8 bytes each; the module reads
+    the canon map on every call, identity or not)."""
     n_t = len(eng.table_rows)
-    return n_t * eng.engram_dim * esize * 2 + 16 + (8 if canon_read else 0)
+    return n_t * eng.engram_dim * esize * 2 + 24
 
 
 def update_batches(eng, dev, n_batches):
@@ -326,7 +327,7 @@ def measure_tiny(dev, steps=32, cycle=4):
         gate_ms = replay_ms([(lambda k=k: gate(k)) for k in range(cycle)], 4)
     M = len(eng.table_rows) * eng.engram_dim
     d = batches[0][2].shape[-1]
-    gbytes = gather_bytes_per_token(eng, 4, False) * T
+    gbytes = gather_bytes_per_token(eng, 4) * T
     flop = 4.0 * M * d * T
     out = {
         "workload": "tiny_forward: 1 engram, orders {2,3}, 16 fp32 tables of 65536 x 64, hidden 1024 "
@@ -371,7 +372,7 @@ def measure_two_engram(dev, steps=3):
     with torch.inference_mode():
         ms = graph_step_ms(chain, steps)
         gather_ms = replay_ms([(lambda k=k: gather(k)) for k in range(2)], 2)
-    gbytes = gather_bytes_per_token(engs[0], 2, not engs[0].identity_canon()) * T
+    gbytes = gather_bytes_per_token(engs[0], 2) * T
     out = {
         "workload": "two_engram_canon: engrams of layers 0 and 29 (seeds 0, 290203), Gemma-scale "
                     "tables each, canon map merging 15% of 262144 ids, batch 8 x 8192 packed Zipf(1.1), "
@@ -513,8 +514,7 @@ def main():
         del src, dst
 
     esize = eng.tables[0].weight.element_size()
-    canon_read = not eng.identity_canon()
-    gbytes = gather_bytes_per_token(eng, esize, canon_read) * T
+    gbytes = gather_bytes_per_token(eng, esize) * T
     gather_gbs = gbytes / (gather_ms * 1e-3) / 1e9
     copy_gbs = 2.0 * (1 << 30) / (copy_ms * 1e-3) / 1e9
     M = len(eng.table_rows) * eng.engram_dim
@@ -561,7 +561,6 @@ def main():
             "frac": gather_gbs / HBM_PEAK_GBS,
             "traffic": GATHER_TRAFFIC_BYTES,
             "bytes_per_launch": gbytes,
-            "canon_read": canon_read,
             "mean_ms": gather_ms,
             "copy_1gib_gbs": copy_gbs,
             "copy_same_size_ms": copy_same_ms,

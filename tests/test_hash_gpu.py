@@ -143,7 +143,7 @@ def test_identity_canon_path_equals_explicit_map():
     # canon=None builds arange(vocab): the kernels' identity path (no canon read) must give the
     # ids of the explicit map, for every op that hashes, including clamped out-of-vocab ids
     eng = _engram(orders=(2, 3, 4), heads=2, dim=64, dtype=torch.bfloat16, vocab=1000)
-    assert eng.identity_canon()
+    assert torch.equal(eng.canon.cpu(), torch.arange(1000))
     ids = torch.randint(-50, 1100, (3, 61), device=DEV)
     pos = torch.cat([torch.arange(30), torch.arange(31)]).to(DEV)
     prev = torch.randint(-1, 1100, (91, 4), dtype=torch.int32, device=DEV)
@@ -159,10 +159,12 @@ def test_identity_canon_path_equals_explicit_map():
     assert torch.equal(first[0], a) and torch.equal(first[1], b)
     assert all(torch.equal(x, y) for x, y in zip(first[2] + first[3], c + d))
     assert np.array_equal(first[0].cpu().numpy(), _oracle_ids(eng, ids, pos[None]))
-    # a write to the buffer turns the identity path off for the module's own calls
-    eng.canon[ids[0, 5].clamp(0, 999)] = 17
-    assert not eng.identity_canon()
+    # the module reads the map on every call: a write through .data (no version bump) is hashed
+    eng.canon.data[ids[0, 5].clamp(0, 999)] = 17
     assert np.array_equal(_stack(eng.hash_ids(ids, pos)), _oracle_ids(eng, ids, pos[None]))
+    want = oracle.hash_prev(prev.cpu().numpy(), eng.mults.cpu().numpy(), eng._table_orders, eng.table_rows,
+                            eng.canon.cpu().numpy(), eng.pad_id)
+    assert np.array_equal(_stack(eng.hash_prev(prev)), want)
 
 
 # ---------------------------------------------------------------- full-size workloads

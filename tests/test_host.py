@@ -117,30 +117,15 @@ def test_bad_gate_and_canon_rejected():
         MicroEngram(model_dim=8, table_size=17, vocab_size=50, canon=torch.arange(49))
 
 
-def test_identity_canon_tracking():
-    # the identity decision follows the buffer: known at construction, carried over .to(), lost
-    # on any in-place write or replacement, re-decided from the values (load_state_dict copies)
-    import copy
-
+def test_module_always_passes_the_canon_map():
+    # the module's hashing reads the canon buffer on every call (no identity shortcut), so a map
+    # written in place, through .data (no version bump) or by load_state_dict is what it hashes
     eng = MicroEngram(64, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3), vocab_size=50)
-    assert eng.identity_canon()
-    eng = eng.to(torch.float64)
-    assert eng._canon_state is not None and eng.identity_canon()
-    eng.canon[3] = 7
-    assert not eng.identity_canon()
-    eng.canon[3] = 3
-    assert eng.identity_canon()
-    sd = eng.state_dict()
-    sd["canon"] = torch.arange(50).flip(0)
-    eng.load_state_dict(sd)
-    assert not eng.identity_canon()
-    merged = MicroEngram(64, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3), vocab_size=50,
-                         canon=torch.arange(50))
-    assert merged._canon_state is None and merged.identity_canon()
-    clone = copy.deepcopy(eng)
-    assert not clone.identity_canon()
-    eng.canon = torch.arange(50)
-    assert eng.identity_canon()
+    canon, _mults, ident = eng._hash_consts(eng.canon.device)
+    assert ident is False and canon is eng.canon
+    eng.canon.data[3] = 7
+    canon, _mults, ident = eng._hash_consts(eng.canon.device)
+    assert ident is False and int(canon[3]) == 7
 
 
 def test_gate_stats_fold_in_order_of_records():
@@ -163,8 +148,8 @@ def test_gate_stats_fold_in_order_of_records():
 
 def test_canon_in_state_dict_like_reference():
     # the reference's test_canon.py:58-66: the map is in the state dict, an old checkpoint
-    # without it still loads (only canon missing), and the map round-trips; a loaded map also
-    # turns off the identity fast path (checked again after a load)
+    # without it still loads (only canon missing), and the map round-trips into what the
+    # module hashes with
     make = lambda canon=None: MicroEngram(model_dim=16, table_size=257, engram_dim=4, num_heads=2,
                                           vocab_size=1000, canon=canon)
     canon = torch.arange(1000)
@@ -175,10 +160,9 @@ def test_canon_in_state_dict_like_reference():
     res = make().load_state_dict(old, strict=False)
     assert list(res.missing_keys) == ["canon"] and not res.unexpected_keys
     e2 = make()
-    assert e2.identity_canon()
     e2.load_state_dict(eng.state_dict())
     assert torch.equal(e2.canon, canon)
-    assert not e2.identity_canon()
+    assert torch.equal(e2._hash_consts(e2.canon.device)[0], canon)
 
 
 def test_ops_route_fake_tensors_to_the_registered_ops():

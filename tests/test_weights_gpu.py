@@ -53,7 +53,7 @@ def test_loaded_engram_forward_bit_exact(tmp_path, fmt, name, dtype):
             "weights": name}
     (tmp_path / W.CONFIG_NAME).write_text(__import__("json").dumps({"engrams": [spec]}))
     got = W.load_engram(str(tmp_path), layer, D, V, device=DEV, dtype=dtype)
-    assert not got.identity_canon()
+    assert torch.equal(got.canon.cpu(), eng.canon.cpu())  # the saved map came back
     ids, pos, hidden = _inputs()
     eng = eng.to(DEV)
     with torch.inference_mode():
