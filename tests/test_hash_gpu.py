@@ -129,6 +129,36 @@ def test_hash_gather_equals_hash_then_gather():
     assert torch.equal(mem, torch.cat(eng.lookup(list(ref_idx.unbind(0))), dim=-1).reshape(100, -1))
 
 
+@pytest.mark.parametrize("n", [1, 700, 1025, 2049, 4089, 4096])
+def test_gathers_across_tokens_per_workgroup(n):
+    # the launches give each workgroup 8 tokens (24 tables), fewer when that would leave under
+    # 512 workgroups (n < 4089: 4, 2 or 1 per workgroup): every size is bit-exact against the
+    # oracle, whole and ragged last workgroups included
+    eng = _engram(orders=(2, 3, 4), heads=8, dim=64, dtype=torch.bfloat16, sizes={2: 4001, 3: 7919, 4: 6007},
+                  canon=torch.randint(0, 1000, (1000,), generator=torch.Generator().manual_seed(n)))
+    gen = torch.Generator().manual_seed(n)
+    ids = torch.randint(-3, 1010, (1, n), generator=gen)
+    pos = torch.arange(n).remainder(517)[None]
+    tabs = [t.weight.detach() for t in eng.tables]
+    tables_np = [t.float().cpu().numpy() for t in tabs]
+    want_idx = _oracle_ids(eng, ids, pos)
+    want_mem = oracle.lookup(tables_np, list(want_idx.reshape(len(tabs), -1)))
+    mem, idx = ops.hash_gather(ids.to(DEV), pos.to(DEV), eng.canon, eng.mults, eng._table_orders,
+                               eng.table_rows, eng.pad_id, tabs, True)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    assert np.array_equal(mem.float().cpu().numpy(), want_mem)
+    got = ops.gather(idx.reshape(len(tabs), -1), tabs)
+    assert np.array_equal(got.float().cpu().numpy(), want_mem)
+    prev = torch.randint(-1, 1010, (n, 4), dtype=torch.int32, generator=gen)
+    prev[::5, 0] = -1
+    want_prev = oracle.hash_prev(prev.numpy(), eng.mults.cpu().numpy(), eng._table_orders, eng.table_rows,
+                                 eng.canon.cpu().numpy(), eng.pad_id)
+    pmem, pidx = ops.hash_prev_gather(prev.to(DEV), eng.canon, eng.mults, eng._table_orders, eng.table_rows,
+                                      eng.pad_id, tabs, True)
+    assert np.array_equal(pidx.cpu().numpy(), want_prev)
+    assert np.array_equal(pmem.float().cpu().numpy(), oracle.lookup(tables_np, list(want_prev)))
+
+
 def test_prev_gather_equals_hash_prev_then_gather():
     eng = _engram(orders=(2, 3, 4), heads=2, dim=64, dtype=torch.bfloat16)
     ids = torch.randint(-1, 1000, (77, 4), dtype=torch.int32, device=DEV)
