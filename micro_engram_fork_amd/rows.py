@@ -97,20 +97,47 @@ def _lookup_keys(idx2d, offs):
     return keys
 
 
+def _table_bounds(uniq_all, count, offs_all):
+    """Each unique key's row in its own table, and [count, bounds of every table in the unique
+    keys] on the device: keys past the count are masked to the largest int64, so a search over
+    the whole output stops at the count. A few launches for all tables; past the count the
+    local rows are unused."""
+    count = count.reshape(1)
+    valid = torch.arange(uniq_all.numel(), device=uniq_all.device) < count
+    masked = torch.where(valid, uniq_all, torch.iinfo(torch.int64).max)
+    offs = offs_all[:-1]
+    local_all = masked - offs[torch.searchsorted(offs, masked, right=True) - 1]
+    return local_all, torch.cat([count, torch.searchsorted(masked, offs_all)])
+
+
 class _KeyPlan:
     """The key half of a row lookup's dedup (unique keys, inverse, segment plan; torch.unique of
-    rows.py:81), made once: at the lookup, or when the launches issued after it are out
-    (key_plans_after)."""
+    rows.py:81) and the tables' bounds in it, made once: at the lookup, or when the launches
+    issued after it are out (key_plans_after). The bounds go to pinned host memory by an
+    asynchronous copy with an event behind it, so the backward's host read waits for the plan
+    only, not for the gate's backward and the weight products queued before it."""
 
     def __init__(self, idx2d, offsets):
         self.idx2d, self.offsets, self.outs = idx2d, offsets, None
 
     def make(self):
         if self.outs is None:
-            keys = _lookup_keys(self.idx2d, _offsets_on(self.offsets, self.idx2d.device)[:-1])
+            offs_all = _offsets_on(self.offsets, self.idx2d.device)
+            keys = _lookup_keys(self.idx2d, offs_all[:-1])
             self.outs = ops.dedup_keys(keys, int(self.offsets[-1]))
+            self.local_all, info = _table_bounds(self.outs[0], self.outs[2], offs_all)
+            self.host = torch.empty(info.shape, dtype=info.dtype, pin_memory=True)
+            self.host.copy_(info, non_blocking=True)
+            self.ready = torch.cuda.Event()
+            self.ready.record()
             self.idx2d = None
         return self.outs
+
+    def bounds(self):
+        """(local rows of the unique keys, [count, table bounds] as host ints)."""
+        self.make()
+        self.ready.synchronize()
+        return self.local_all, self.host.tolist()
 
 
 _PLANS = threading.local()
@@ -168,21 +195,16 @@ class _RowLookup(torch.autograd.Function):
         D = ctx.shapes[0][0][1]
         offs_all = _offsets_on(ctx.offsets, idx2d.device)
         offs = offs_all[:-1]
-        if ctx.plan is not None:  # the key half ran in the forward
+        if ctx.plan is not None:  # the key half and the bounds ran in the forward
             uniq_all, inv, count, plan = ctx.plan.make()
-            ctx.plan = None
             outs = [uniq_all, inv, count, ops.dedup_sums(plan, count, grad.reshape(n * nt, D))]
+            local_all, host = ctx.plan.bounds()
+            ctx.plan = None
         else:
             outs = ops.dedup(_lookup_keys(idx2d, offs), int(ctx.offsets[-1]), grad.reshape(n * nt, D))
-        # one host read for the unique count and every table's bounds: keys past the count are
-        # masked to the largest int64, so a search over the whole output stops at the count
-        count = outs[2].reshape(1)
-        valid = torch.arange(outs[0].numel(), device=idx2d.device) < count
-        masked = torch.where(valid, outs[0], torch.iinfo(torch.int64).max)
-        # every unique key's row in its own table, in a few launches for all tables, queued
-        # before the host read (past the count the values are unused)
-        local_all = masked - offs[torch.searchsorted(offs, masked, right=True) - 1]
-        host = torch.cat([count, torch.searchsorted(masked, offs_all)]).tolist()
+            # one host read for the unique count and every table's bounds
+            local_all, info = _table_bounds(outs[0], outs[2], offs_all)
+            host = info.tolist()
         cnt, bounds = host[0], host[1:]
         # each table's slice of the unique rows and sums (bounds[0] = 0, bounds[nt] = count)
         sizes = [bounds[k + 1] - bounds[k] for k in range(nt)]
