@@ -504,7 +504,7 @@ def main():
         n_lookups = ubatches[0][0].numel()
         n_uniq = float(np.mean([u[4] for u in ubatches]))
         del ubatches, exp_avgs, exp_avg_sqs
-    train_ms = training_step_ms(dev, batches, steps=10, warmup=3)
+    train_ms = training_step_ms(dev, batches, steps=30, warmup=10)
     tiny = measure_tiny(dev)
     two = measure_two_engram(dev)
     with torch.inference_mode():
