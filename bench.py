@@ -158,6 +158,9 @@ def training_step_ms(dev, batches, steps, warmup):
 
     for k in range(warmup):
         step(k)
+    # read the gate statistics once, as a trainer's log step does (the first fold of a process
+    # also loads its reduction kernels, ~10 ms once); fewer than 32 timed steps then fold none
+    eng.pop_gate_stats()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(steps):
