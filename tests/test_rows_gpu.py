@@ -401,6 +401,50 @@ def test_key_plan_after_gate_matches_plan_at_lookup():
         assert np.array_equal(got[1][k][1].cpu().numpy().view(np.int32), acc.view(np.int32))
 
 
+def test_two_chained_engrams_one_backward():
+    # two engrams in one graph (the second reads the first's output): each forward leaves its
+    # key plan and its tables' bounds (copied to host memory behind an event) after its gate,
+    # and the one backward reads both, the second engram's first; the sparse gradients equal
+    # those of the same graph with the plans made at the lookups, and the oracle's dedup of
+    # each memory gradient
+    engs = [MicroEngram(model_dim=32, table_size=97, engram_dim=8, num_heads=2, orders=(2, 3),
+                        vocab_size=500, seed=s).to(DEV) for s in (7, 8)]
+    shards = [e.shard_rows(0, 1, device=DEV) for e in engs]
+    for sh in shards:
+        for s in sh:
+            s._sparse_rows = True
+    ids = torch.randint(0, 500, (2, 48), device=DEV)
+    idxs = [e.hash_ids(ids) for e in engs]
+    hidden = torch.randn(2, 48, 32, device=DEV)
+    gout = torch.randn(2, 48, 32, device=DEV)
+    got = []
+    for deferred in (True, False):
+        for sh in shards:
+            for s in sh:
+                s.sparse_grad = None
+        x = hidden.clone().requires_grad_(True)
+        mems = []
+        for e, idx in zip(engs, idxs):
+            if deferred:
+                x = e.inject(x, idx)
+            else:
+                mem = e._mem_grad(idx)
+                mem.retain_grad()
+                mems.append(mem)
+                x = e._gate(x, mem, None)
+        x.backward(gout)
+        got.append([[(s.sparse_grad[0].clone(), s.sparse_grad[1].clone()) for s in sh] for sh in shards])
+    D = 8
+    for e_i, (sh, mem) in enumerate(zip(shards, mems)):
+        for k in range(len(sh)):
+            (ua, ga), (ub, gb) = got[0][e_i][k], got[1][e_i][k]
+            assert torch.equal(ua, ub) and torch.equal(ga.view(torch.int32), gb.view(torch.int32))
+            u, _, acc = oracle.dedup(idxs[e_i][k].reshape(-1).cpu().numpy(),
+                                     mem.grad[:, k * D:(k + 1) * D].cpu().numpy())
+            assert np.array_equal(ub.cpu().numpy(), u)
+            assert np.array_equal(gb.cpu().numpy().view(np.int32), acc.view(np.int32))
+
+
 def _clip_engram(dtype, sparse):
     eng = MicroEngram(model_dim=16, table_size=64, engram_dim=8, num_heads=2, orders=(2,), vocab_size=50,
                       seed=4)
