@@ -129,7 +129,7 @@ class _KeyPlan:
             self.host = torch.empty(info.shape, dtype=info.dtype, pin_memory=True)
             self.host.copy_(info, non_blocking=True)
             self.ready = torch.cuda.Event()
-            self.ready.record()
+            self.ready.record(torch.cuda.current_stream(info.device))  # the copy's stream
             self.idx2d = None
         return self.outs
 
