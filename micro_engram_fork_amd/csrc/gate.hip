@@ -1561,6 +1561,15 @@ extern "C" int me_gate_backward_workspace_size(int64_t n, int64_t model_dim, siz
     return ME_OK;
 }
 
+// Zeroes two fp32 vectors of n values (the scale gradients of an empty batch).
+__global__ __launch_bounds__(256) void zero_two_f32_kernel(float *a, float *b, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) {
+        a[i] = 0.0f;
+        b[i] = 0.0f;
+    }
+}
+
 extern "C" int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
                                 const void *mem, int64_t mem_dim, const void *w_key,
                                 const void *w_value, int dtype, const void *q_scale_delta,
@@ -1573,10 +1582,12 @@ extern "C" int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n,
     if (n == 0) {
         // no tokens: the scale gradients are zero
         if (gate_mode == ME_GATE_SCALAR_SQRT && grad_q_scale != nullptr && grad_k_scale != nullptr) {
-            hipStream_t s0 = as_stream(stream);
-            if (hipMemsetAsync(grad_q_scale, 0, model_dim * 4, s0) != hipSuccess ||
-                hipMemsetAsync(grad_k_scale, 0, model_dim * 4, s0) != hipSuccess)
-                return check_launch("me_gate_backward (zero scale gradients)");
+            // a fill kernel, not hipMemsetAsync: a captured backward then records no memset node
+            ME_CHECK_ARG(model_dim >= 1 && model_dim < (int64_t{1} << 30), "bad model_dim");
+            const unsigned blocks = static_cast<unsigned>(ceil_div(model_dim, 256));
+            hipLaunchKernelGGL(zero_two_f32_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                               grad_q_scale, grad_k_scale, model_dim);
+            return check_launch("me_gate_backward (zero scale gradients)");
         }
         return ME_OK;
     }

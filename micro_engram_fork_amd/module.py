@@ -247,7 +247,11 @@ class MicroEngram(nn.Module):
     @staticmethod
     def _stacked_idx(idx):
         """[n_tables, N] int64 view of the per-table ids: no copy when they are the rows of one
-        buffer (what hash_ids / hash_prev return), else a stacked copy."""
+        buffer (what hash_ids / hash_prev return), else a stacked copy. Under torch.compile the
+        stack is what gets traced (storage addresses are not traceable); the compiler sees the
+        unbind of one buffer followed by its stack."""
+        if torch.compiler.is_compiling():
+            return torch.stack([i.reshape(-1).long() for i in idx])
         first = idx[0]
         n = first.numel()
         storage = first.untyped_storage().data_ptr()
@@ -297,7 +301,9 @@ class MicroEngram(nn.Module):
     def lookup(self, idx):
         """The table rows for the hashed ids: list of n_tables tensors [*idx shape, D]
         (module.py:146-154). Row-sharded tables go through the server's lookup or the
-        differentiable row lookup (sparse row gradients, micro_engram/rows.py:150-161)."""
+        differentiable row lookup (sparse row gradients, micro_engram/rows.py:150-161). Plain
+        tables carry their gradients when grad mode is on and a table requires one, as
+        nn.Embedding does (the row lookup: dense table gradients through the dedup kernels)."""
         if self.row_shards is not None:
             if self.row_lookup_fn is not None:
                 return self.row_lookup_fn(self, idx)
@@ -305,9 +311,18 @@ class MicroEngram(nn.Module):
 
             return row_lookup(self, idx)
         shape = tuple(idx[0].shape)
-        mem = self._mem(idx)
+        if torch.is_grad_enabled() and any(t.weight.requires_grad for t in self.tables):
+            mem = self._mem_grad(idx)
+        else:
+            mem = self._mem(idx)
         D = self.engram_dim
         return [mem[:, k * D:(k + 1) * D].reshape(*shape, D) for k in range(len(idx))]
+
+    def _lookup_replaced(self):
+        """True when `lookup` is not this class's own: set on the instance (as the reference's
+        tests do, test_zero_order.py:84-88) or overridden by a subclass. inject and forward then
+        read the rows through it, as module.py:233 does."""
+        return "lookup" in self.__dict__ or type(self).lookup is not MicroEngram.lookup
 
     # -------------------------------------------------------------------------------- inject
     def _needs_grad(self, hidden):
@@ -332,7 +347,10 @@ class MicroEngram(nn.Module):
         q = self.q_scale.detach() if sqrt else None
         k = self.k_scale.detach() if sqrt else None
         n_tok = hidden.numel() // hidden.shape[-1]
-        limit = self.few_tokens_max if mem.dtype == torch.bfloat16 else self.few_tokens_max_fp32
+        if mem.dtype == torch.bfloat16:
+            limit = self.few_tokens_max
+        else:  # also bounded by the fp32 K|V rows the few-token path writes ([N, 2d])
+            limit = min(self.few_tokens_max_fp32, self.few_tokens_kv_bytes // (8 * hidden.shape[-1]))
         if n_tok <= limit:
             outs = ops.gate_residual_rows(hidden, mem, self.key.weight.detach(), self.value.weight.detach(),
                                           q, k, mode, keep, self.training)
@@ -350,13 +368,20 @@ class MicroEngram(nn.Module):
     # bf16): 256 tokens 33 us against 73, 1024 tokens 61 against 74, 1536 tokens 88 against 76.
     # fp32 engrams: the fused kernel's fp32 tiles are 256 x 256 on 32x32x2 MFMAs, so a 2048-token
     # batch (model dim 1024) gives it 32 tiles per pass (538 us) and the few-token path (72 us for
-    # the projection) stays ahead far longer.
+    # the projection) stays ahead far longer. That range was measured at model dim 1024 only, so
+    # for fp32 the token count is also capped by the bytes of the [N, 2d] fp32 K|V rows the
+    # few-token path writes: 128 MiB, i.e. 16384 tokens at model dim 1024, 3120 at 5376.
     few_tokens_max = 1024
     few_tokens_max_fp32 = 16384
+    few_tokens_kv_bytes = 128 << 20
 
     def inject(self, hidden, idx, keep=None):
         """hidden + gated memory of the rows `idx` (module.py:228-261); keep: optional [N] bool,
         False leaves that token unchanged. Returns a new tensor."""
+        if self._lookup_replaced():
+            rows = self.lookup(idx)
+            mem = torch.cat(rows, dim=-1)
+            return self._gate(hidden, mem.reshape(-1, mem.shape[-1]), keep)
         if not self._needs_grad(hidden):
             return self._gate(hidden, self._mem(idx), keep)
         from .rows import key_plans_after
@@ -366,8 +391,10 @@ class MicroEngram(nn.Module):
 
     def forward(self, hidden, input_ids, position_ids=None):
         """inject(hidden, hash_ids(input_ids, position_ids)) (module.py:263-265); without
-        gradients the hashing and the gather run as one fused kernel."""
-        if self._needs_grad(hidden) or (self.row_lookup_fn is not None and self.row_shards is not None):
+        gradients the hashing and the gather run as one fused kernel (unless `lookup` has been
+        replaced, which then reads the rows)."""
+        if (self._needs_grad(hidden) or self._lookup_replaced()
+                or (self.row_lookup_fn is not None and self.row_shards is not None)):
             return self.inject(hidden, self.hash_ids(input_ids.to(hidden.device), position_ids))
         return self._gate(hidden, self.hashed_memory(input_ids, position_ids, hidden.device), None)
 

@@ -11,7 +11,6 @@ import functools
 from typing import List, Optional, Sequence
 
 import torch
-from torch._subclasses.fake_tensor import FakeTensor
 
 from . import _lib
 from ._lib import ME_BF16, ME_F32, ME_I32, ME_I64, ME_U8, call, i32_array, i64_array, ptr_array
@@ -52,21 +51,42 @@ def stream_of(device):
     return torch._C._cuda_getCurrentRawStream(index)
 
 
+_PLAIN_TENSORS = (torch.Tensor, torch.nn.Parameter)
+
+
+def _plain(value):
+    """True for a plain eager tensor (or parameter), a list/tuple of them, or a non-tensor."""
+    if isinstance(value, torch.Tensor):
+        return type(value) in _PLAIN_TENSORS
+    if isinstance(value, (list, tuple)):
+        return all(_plain(v) for v in value)
+    return True
+
+
+def _direct_call(args, kwargs):
+    """Whether a call may skip the op's dispatch: nothing is tracing (dynamo), no dispatch mode
+    is active (make_fx, FlopCounterMode, debug or recording modes see only the dispatcher) and
+    every tensor argument is a plain tensor (fake tensors and other subclasses need the op)."""
+    return (not torch.compiler.is_compiling() and torch._C._len_torch_dispatch_stack() == 0
+            and all(_plain(a) for a in args) and all(_plain(v) for v in kwargs.values()))
+
+
 def _custom_op(name):
     """Registers the decorated function as the custom op micro_engram_amd::<name> (what
     torch.compile traces and what a captured graph replays; its fake is added with
-    .register_fake) and returns a function that calls the implementation itself when nothing is
-    being traced: the op's dispatch costs ~20 us of host time per call, and an eager training
-    step is bound by the rate at which the host issues its launches. Under tracing, or for fake
-    tensors, calls go through the op."""
+    .register_fake) and returns a function that calls the implementation itself for plain eager
+    tensors when nothing traces or intercepts the call: the op's dispatch costs ~20 us of host
+    time per call, and an eager training step is bound by the rate at which the host issues its
+    launches. Everything else (tracing, dispatch modes, fake tensors or other tensor subclasses)
+    goes through the op."""
     def wrap(fn):
         op = torch.library.custom_op(f"micro_engram_amd::{name}", mutates_args=())(fn)
 
         @functools.wraps(fn)
         def dispatch(*args, **kwargs):
-            if torch.compiler.is_compiling() or (args and isinstance(args[0], FakeTensor)):
-                return op(*args, **kwargs)
-            return fn(*args, **kwargs)
+            if _direct_call(args, kwargs):
+                return fn(*args, **kwargs)
+            return op(*args, **kwargs)
 
         dispatch.op = op
         dispatch.register_fake = op.register_fake

@@ -57,7 +57,7 @@ def _spans(tensors):
     for t in tensors:
         if t.dtype == torch.float32 and t.is_contiguous() and spans:
             last = spans[-1]
-            if (last.dtype == torch.float32 and
+            if (last.dtype == torch.float32 and last.dim() == 1 and last.is_contiguous() and
                     last.untyped_storage().data_ptr() == t.untyped_storage().data_ptr() and
                     last.data_ptr() + last.numel() * 4 == t.data_ptr()):
                 spans[-1] = last.as_strided((last.numel() + t.numel(),), (1,), last.storage_offset())

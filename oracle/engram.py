@@ -10,7 +10,11 @@ hash_ids                 micro_engram/module.py:183-205                   exact 
                                                                           test_vllm_ids.py:68-83
 hash_prev                micro_engram/module.py:207-226                   hash_prev == hash_ids
                                                                           (test_vllm_ids.py:68-83)
+hash_ids_torch           micro_engram/module.py:183-205 as torch ops      == hash_ids (C), bit for bit
+hash_prev_torch          micro_engram/module.py:207-226 as torch ops      == hash_prev (C), bit for bit
 lookup                   module.py:146-154, micro_engram_vllm/tp.py:20-39 numpy fancy indexing identity
+lookup_torch             module.py:146-154 (F.embedding + cat)            == lookup (tests of the bench's
+                                                                          baseline inputs)
 inject                   micro_engram/module.py:228-261                   test_oracle_inject.py: value=0
                                                                           no-op and keep mask
                                                                           (test_gate.py:24-27, 122-130);
@@ -26,6 +30,7 @@ inject_backward          autograd of micro_engram/module.py:239-261       torch.
                                                                           of inject in float64
 dedup                    micro_engram/rows.py:81, 117-118, 137-147        brute-force Python loop on tiny
                                                                           inputs; uniq[inv] == keys
+dedup_torch              micro_engram/rows.py:81, 117-118 as torch ops    the same brute force, bit for bit
 philox4x32_10            Salmon et al. 2011 (Random123)                   published known-answer vectors
 stochastic_bf16          micro_engram/optim.py:33-44                      exhaustive 2^16-noise count;
                                                                           fp32 pass-through, inf kept
@@ -177,6 +182,24 @@ def hash_ids_torch(input_ids, mults, orders, rows, canon, pad_id, position_ids=N
     return torch.stack(out)
 
 
+def hash_prev_torch(ids, mults, orders, rows, canon, pad_id):
+    """hash_prev as torch-CPU tensor ops, step for step as module.py:207-226 writes them (canon
+    after a clamp, missing predecessors (-1) as the raw pad id, the int64 sum of products, then
+    % P % rows): the CPU baseline of the serving decode step. Returns int64 [n_tables, N]."""
+    ids = torch.as_tensor(ids).long()
+    canon = torch.as_tensor(canon).long()
+    mults = torch.as_tensor(mults).long()
+    merged = canon[ids.clamp(0, canon.numel() - 1)]
+    merged = torch.where(ids >= 0, merged, torch.full_like(merged, pad_id))
+    out = []
+    for k, n in enumerate(orders):
+        x = merged[:, 0] * mults[k, 0]
+        for i in range(1, n):
+            x = x + merged[:, i] * mults[k, i]
+        out.append((x % PRIME) % int(rows[k]))
+    return torch.stack(out)
+
+
 def hash_bigint(tokens, mults_row, order, rows):
     """One n-gram row id in Python's arbitrary-precision integers: sum(tok_i * mult_i) % P % rows.
     Exact whenever the int64 sum does not wrap (|tokens| < 2^31)."""
@@ -291,6 +314,16 @@ def dedup(keys, grads):
     acc = np.zeros((uniq.size,) + grads.shape[1:], dtype=np.float32)
     np.add.at(acc, inv, grads)  # unbuffered, in index order: ((0 + g_a) + g_b) + ...
     return uniq, inv.astype(np.int64), acc
+
+
+def dedup_torch(keys, grads):
+    """dedup as the reference's torch-CPU ops (rows.py:81, 117-118): torch.unique(return_inverse)
+    and zeros().index_add_() of the fp32 gradient rows. The CPU baseline of the sparse update."""
+    uniq, inv = torch.unique(torch.as_tensor(keys).long(), return_inverse=True)
+    g = torch.as_tensor(grads).float()
+    acc = torch.zeros((uniq.numel(),) + tuple(g.shape[1:]), dtype=torch.float32)
+    acc.index_add_(0, inv, g)
+    return uniq, inv, acc
 
 
 # -------------------------------------------------------------------------------------- clip

@@ -234,3 +234,40 @@ def test_backward_gemma_prefill_full():
     rt.zero_grad()
     del eng, got, shards
     torch.cuda.empty_cache()
+
+
+def test_empty_batch_zeroes_the_scale_gradients_in_a_graph():
+    # no tokens: the scale-delta gradients are zero, written by a fill kernel (so a captured
+    # backward records no memset node); checked eagerly and on every replay of a captured call
+    from micro_engram_fork_amd import _lib
+    from micro_engram_fork_amd._lib import ME_BF16, ME_F32, ME_GATE_SCALAR_SQRT
+
+    d = 1000
+    gq = torch.full((d,), 7.0, device=DEV)
+    gk = torch.full((d,), 7.0, device=DEV)
+    dummy = torch.zeros(64, dtype=torch.bfloat16, device=DEV)
+    deltas = torch.zeros(d, device=DEV)
+
+    def call():
+        p = dummy.data_ptr()
+        _lib.call("me_gate_backward", p, ME_BF16, 0, d, p, 16, p, p, ME_BF16, deltas.data_ptr(),
+                  deltas.data_ptr(), ME_F32, ME_GATE_SCALAR_SQRT, None, p, None, p, p, p,
+                  gq.data_ptr(), gk.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream)
+
+    call()
+    torch.cuda.synchronize()
+    assert not gq.any() and not gk.any()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            call()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        gq.fill_(7.0)
+        gk.fill_(-3.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert not gq.any() and not gk.any()

@@ -204,3 +204,29 @@ def test_torch_restatement_equals_c_oracle(seed):
     want = oracle.hash_ids(ids, mults, orders, rows, canon, pad, position_ids=pos)
     got = oracle.hash_ids_torch(ids, mults, orders, rows, canon, pad, position_ids=pos)
     assert np.array_equal(got.numpy(), want)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_torch_hash_prev_equals_c_oracle(seed):
+    # the decode baseline's torch-op hash_prev gives the C oracle's row ids bit for bit, with
+    # missing predecessors (-1), out-of-range ids (clamped) and a negative pad id
+    rng = np.random.Generator(np.random.PCG64(200 + seed))
+    V = 700
+    mults = oracle.make_mults(seed, 6, 4)
+    orders, rows = [2, 2, 3, 3, 4, 4], [1009, 97, 257, 2**31 + 11, 4099, 65536]
+    canon = rng.integers(-50, V, size=V)
+    mat = rng.integers(-1, V + 40, size=(57, 5))
+    mat[rng.random((57, 5)) < 0.2] = -1
+    pad = int(rng.integers(-9, V))
+    want = oracle.hash_prev(mat, mults, orders, rows, canon, pad)
+    got = oracle.hash_prev_torch(mat, mults, orders, rows, canon, pad)
+    assert np.array_equal(got.numpy(), want)
+
+
+def test_lookup_torch_equals_lookup():
+    # F.embedding + cat (the CPU baselines' lookup) == the numpy fancy-index lookup
+    rng = np.random.Generator(np.random.PCG64(3))
+    tables = [rng.standard_normal((r, 8)).astype(np.float32) for r in (31, 57, 12)]
+    idx = [rng.integers(0, t.shape[0], size=40) for t in tables]
+    got = oracle.lookup_torch([torch.from_numpy(t) for t in tables], idx)
+    assert np.array_equal(got.numpy(), oracle.lookup(tables, idx))

@@ -97,6 +97,19 @@ def test_dedup_matches_torch_unique_index_add():
     assert np.array_equal(a.view(np.int32), acc.numpy().view(np.int32))
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_dedup_torch_equals_bruteforce(seed):
+    # the sparse-update baseline's torch-op dedup: the brute force's unique keys, inverse and
+    # fp32 sums bit for bit
+    rng = np.random.Generator(np.random.PCG64(40 + seed))
+    keys = rng.integers(0, 40, size=300) * rng.integers(1, 5000)
+    grads = (rng.standard_normal((300, 6)) * 10 ** rng.uniform(-4, 2, size=(300, 1))).astype(np.float32)
+    u, inv, acc = oracle.dedup_torch(keys, grads)
+    bu, binv, bacc = _dedup_brute(keys, grads)
+    assert np.array_equal(u.numpy(), bu) and np.array_equal(inv.numpy(), binv)
+    assert np.array_equal(acc.numpy().view(np.int32), bacc.view(np.int32))
+
+
 def test_dedup_golden_fixture():
     f = np.load(os.path.join(os.path.dirname(__file__), "golden", "dedup_small.npz"))
     u, inv, acc = oracle.dedup(f["keys"], f["grads"])

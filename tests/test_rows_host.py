@@ -21,3 +21,20 @@ def test_spans_keep_other_dtypes_and_gaps_apart():
     buf = torch.zeros(10, dtype=torch.float32)
     parts = [buf[0:4], buf[5:9], torch.zeros(3, dtype=torch.bfloat16)]
     assert [s.numel() for s in _spans(parts)] == [4, 4, 3]
+
+
+def test_spans_never_extend_a_strided_span():
+    # a strided (non-contiguous) gradient followed by a contiguous one that starts where the
+    # strided view's last element would end if it were dense: they stay apart, so the clip's
+    # norm and scaling touch exactly the gradients' own elements
+    buf = torch.arange(40, dtype=torch.float32)
+    strided = buf[:20].view(5, 4)[:, :2]          # 10 elements, not contiguous
+    after = buf[10:14]                            # starts at strided.data_ptr() + 10 * 4
+    assert not strided.is_contiguous()
+    assert strided.data_ptr() + strided.numel() * 4 == after.data_ptr()
+    spans = _spans([strided, after])
+    assert len(spans) == 2
+    assert torch.equal(spans[0], strided) and torch.equal(spans[1], after)
+    # a contiguous 1-D span followed by its neighbour still merges
+    merged = _spans([buf[:6], buf[6:9]])
+    assert len(merged) == 1 and torch.equal(merged[0], buf[:9])

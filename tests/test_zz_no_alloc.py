@@ -86,12 +86,23 @@ def test_noalloc_gemma_decode_shape():
 
 
 def test_noalloc_refuses_more_than_its_scratch():
-    # 14,365 tokens at model dim 5376 need more than the 4 MiB array: an error, nothing launched
-    n, d = 14_365, 5376
+    # 14,365 tokens at model dim 5376 need more than the 4 MiB array: an error, nothing launched.
+    # The operands are real device tensors of that shape, so a regressed size check could only
+    # give a wrong result, never an access outside an allocation.
+    n, d, m = 14_365, 5376, 1536
     need = ops.gate_workspace_bytes(n, d)
     assert need > 4 << 20 >= ops.gate_workspace_bytes(n - 1, d)
-    fake = 1 << 20  # never dereferenced: the size check comes first
+    hidden = torch.zeros(n, d, dtype=torch.bfloat16, device=DEV)
+    mem = torch.zeros(n, m, dtype=torch.bfloat16, device=DEV)
+    wk = torch.zeros(d, m, dtype=torch.bfloat16, device=DEV)
+    wv = torch.zeros(d, m, dtype=torch.bfloat16, device=DEV)
+    dq = torch.zeros(d, device=DEV)
+    dk = torch.zeros(d, device=DEV)
+    out = torch.full_like(hidden, 1.5)
     stream = torch.cuda.current_stream().cuda_stream
     with pytest.raises(_lib.EngramLibError, match="static scratch"):
-        _lib.call("me_gate_residual_noalloc", fake, ME_BF16, n, d, fake, 1536, fake, fake, ME_BF16,
-                  fake, fake, ME_F32, ME_GATE_SCALAR_SQRT, None, fake, None, None, stream)
+        _lib.call("me_gate_residual_noalloc", hidden.data_ptr(), ME_BF16, n, d, mem.data_ptr(), m,
+                  wk.data_ptr(), wv.data_ptr(), ME_BF16, dq.data_ptr(), dk.data_ptr(), ME_F32,
+                  ME_GATE_SCALAR_SQRT, None, out.data_ptr(), None, None, stream)
+    torch.cuda.synchronize()
+    assert bool((out == 1.5).all())  # nothing was written
