@@ -20,7 +20,13 @@ all inputs already in HBM. Prints one JSON line:
                 stream (the rocprofv3 kernel trace of this script's step sequence agrees).
                 copy_1gib_gbs: a 1 GiB device copy, the known-size kernel that calibrates the
                 HBM byte counters; copy_same_size: a device copy of the gather's output size
-                (25 MB read + 25 MB written), the cost of the same bytes with no hashing
+                (25 MB read + 25 MB written), the cost of the same bytes with no hashing;
+                copy_same_size_nt: the same copy by a non-temporal 16-byte copy kernel (the
+                fastest sequential copy of these bytes measured here); random_rows_same_size:
+                the gather's access shape (random 128-byte rows of the same tables, written
+                concatenated in token order) with row ids from integer arithmetic, so no
+                dependent load precedes the row reads -- what random row reads of this size
+                sustain; gather_over_random_rows = its time / the gather's
   roofline_gate the K/V projection + gate + residual kernels: 4 * M * d FLOP per token / their
                 mean duration (graph replay, as above), against 2.5 PFLOP/s dense bf16
   serving_decode  a decode step of 256 one-token sequences on the same engram (hash_prev +
@@ -44,8 +50,15 @@ all inputs already in HBM. Prints one JSON line:
                 tokens/s and the gather's HBM roofline
   cpu_baseline  the reference path restated in torch-CPU ops (the oracle) on the same batch:
                 hash on all tokens, lookup + inject on a sample, medians of 5 runs
+  cpu_baseline_configs  the same restatement for the other workloads, each beside the GPU
+                figure in its unit (gpu_value): tiny_forward (the whole fp32 forward),
+                serving_decode (hash_prev + lookup + inject of one 256-token step),
+                two_engram_canon (both engrams' hashes on all tokens, the chained lookups and
+                injects on a sample), sparse_update (torch.unique + index_add_ + each table's
+                row-wise Adam with stochastic rounding, one batch's 196,608 lookups)
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -117,6 +130,14 @@ def update_batches(eng, dev, n_batches):
     return out, offs[-1]
 
 
+def key_bound_offsets(eng):
+    """First key of every table in the concatenated key space, and the total (len n_tables + 1)."""
+    offs = [0]
+    for r in eng.table_rows:
+        offs.append(offs[-1] + r)
+    return offs
+
+
 def update_bytes(n_lookups, n_uniq, dim, esize):
     """Algorithmic bytes of one sparse update, in three parts.
     Key plan (in the forward, from the row ids): read the int64 keys; write the unique keys,
@@ -184,32 +205,89 @@ def cpu_model():
     return None
 
 
-def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5):
+def calib_lib():
+    """The benchmark's calibration kernels (micro_engram_fork_amd/csrc/calib), through ctypes."""
+    from micro_engram_fork_amd._build import CALIB_LIB_PATH
+
+    lib = ctypes.CDLL(CALIB_LIB_PATH)
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    lib.me_calib_copy_nt.argtypes = [P, P, I64, ctypes.c_int, P]
+    lib.me_calib_random_rows.argtypes = [P, P, ctypes.c_int, P, I64, ctypes.c_uint32, P]
+    return lib
+
+
+def calib_ok(status):
+    if status != 0:
+        raise RuntimeError(f"calibration kernel launch failed ({status})")
+
+
+def _oracle():
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+
+    return oracle
+
+
+def cpu_threads():
+    """torch intra-op threads for the CPU baselines: the host cores this process may use."""
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def median_s(fn, runs=5):
+    """Median wall-clock seconds of `runs` calls of fn after one warm-up call."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+class CpuEngram:
+    """An engram's tensors copied to host memory, for the torch-CPU restatement of the
+    reference path (the oracle's functions): tables, key / value weights, scale deltas, hash
+    constants."""
+
+    def __init__(self, eng):
+        self.tables = [t.weight.detach().cpu() for t in eng.tables]
+        self.wk, self.wv = eng.key.weight.detach().cpu(), eng.value.weight.detach().cpu()
+        self.dq, self.dk = eng.q_scale.detach().cpu(), eng.k_scale.detach().cpu()
+        self.mults, self.canon = eng.mults.cpu(), eng.canon.cpu()
+        self.orders, self.rows, self.pad_id = eng._table_orders, eng.table_rows, eng.pad_id
+
+    def hash_ids(self, ids, pos):
+        return _oracle().hash_ids_torch(ids, self.mults, self.orders, self.rows, self.canon,
+                                        self.pad_id, position_ids=pos)
+
+    def hash_prev(self, ids):
+        return _oracle().hash_prev_torch(ids, self.mults, self.orders, self.rows, self.canon,
+                                         self.pad_id)
+
+    def inject(self, hidden, idx):
+        """lookup + cat + inject (module.py:146-154, 228-261) of hidden [n, d] with the row ids
+        idx [n_tables, n]."""
+        oracle = _oracle()
+        mem = oracle.lookup_torch(self.tables, list(idx))
+        return oracle.inject(hidden, mem, self.wk, self.wv, "scalar_sqrt", self.dq, self.dk)
+
+
+def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5, cpu_eng=None):
     """The reference path restated op for op in torch on the CPU (the oracle): hash_ids as
     torch tensor ops (module.py:183-205) on the whole batch, then F.embedding lookups + inject
     (module.py:146-154, 228-261) on a token sample; each timed as the median of `runs` runs
     after one warm-up, with torch's intra-op threads = the host cores this process may use."""
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    import oracle
-
-    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
-    torch.set_num_threads(threads)
-    tables = [t.weight.detach().cpu() for t in eng.tables]
-    wk, wv = eng.key.weight.detach().cpu(), eng.value.weight.detach().cpu()
-    dq, dk = eng.q_scale.detach().cpu(), eng.k_scale.detach().cpu()
+    oracle = _oracle()
+    threads = cpu_threads()
+    ce = cpu_eng or CpuEngram(eng)
+    tables, wk, wv, dq, dk = ce.tables, ce.wk, ce.wv, ce.dq, ce.dk
     ids_c, pos_c = ids.cpu(), pos.cpu()
-    mults, canon = eng.mults.cpu(), eng.canon.cpu()
+    mults, canon = ce.mults, ce.canon
     h_all = hidden.reshape(-1, hidden.shape[-1]).cpu()
     T = h_all.shape[0]
-
-    def median_s(fn):
-        fn()  # warm-up
-        times = []
-        for _ in range(runs):
-            t0 = time.perf_counter()
-            fn()
-            times.append(time.perf_counter() - t0)
-        return float(np.median(times))
+    median_s_ = lambda fn: median_s(fn, runs)
 
     hash_out = {}
 
@@ -217,7 +295,7 @@ def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5):
         hash_out["idx"] = oracle.hash_ids_torch(ids_c, mults, eng._table_orders, eng.table_rows,
                                                 canon, eng.pad_id, position_ids=pos_c)
 
-    hash_s_per_tok = median_s(hash_all) / T
+    hash_s_per_tok = median_s_(hash_all) / T
     idx = hash_out["idx"].reshape(len(tables), -1)
 
     def run(sample):
@@ -232,12 +310,107 @@ def cpu_baseline(eng, ids, pos, hidden, target_s, runs=5):
     per_tok = (time.perf_counter() - t0) / probe.numel()
     n = int(min(T, max(128, target_s / max(per_tok, 1e-9) / (runs + 1))))
     sample = torch.from_numpy(np.sort(rng.choice(T, n, replace=False)))
-    per_tok = median_s(lambda: run(sample)) / n + hash_s_per_tok
+    per_tok = median_s_(lambda: run(sample)) / n + hash_s_per_tok
     return {"value": 1.0 / per_tok, "unit": "tokens/s", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(),
             "sample": f"hash_ids as torch-CPU ops on all {T} tokens, then lookup + inject on {n} of "
                       f"them; each the median of {runs} runs after 1 warm-up; per-token times "
                       f"added"}
+
+
+def _baseline(value, unit, threads, sample, **extra):
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "sample": sample, **extra}
+
+
+def cpu_baseline_tiny(eng, batch, runs=5):
+    """The tiny fp32 forward restated in torch-CPU ops: hash_ids + lookup + inject of all its
+    tokens (module.py:183-205, 146-154, 228-261), the median of `runs` runs."""
+    threads = cpu_threads()
+    ce = CpuEngram(eng)
+    ids, pos, hidden = (t.cpu() for t in batch)
+    h = hidden.reshape(-1, hidden.shape[-1])
+    T = h.shape[0]
+    sec = median_s(lambda: ce.inject(h, ce.hash_ids(ids, pos).reshape(len(ce.tables), -1)), runs)
+    return _baseline(T / sec, "tokens/s", threads,
+                     f"the whole forward of all {T} tokens; median of {runs} runs after 1 warm-up",
+                     ms_per_forward=sec * 1e3)
+
+
+def cpu_baseline_decode(ce, ids, hidden, runs=5):
+    """A serving decode step restated in torch-CPU ops: hash_prev + lookup + inject
+    (module.py:207-226, 146-154, 228-261) of its tokens on the host copy of the tables."""
+    threads = cpu_threads()
+    ids, hidden = ids.cpu(), hidden.cpu()
+    sec = median_s(lambda: ce.inject(hidden, ce.hash_prev(ids)), runs)
+    n = ids.shape[0]
+    return _baseline(n / sec, "tokens/s", threads,
+                     f"one whole decode step of {n} tokens; median of {runs} runs after 1 warm-up",
+                     step_ms=sec * 1e3)
+
+
+def cpu_baseline_two_engram(engs, ids, pos, hidden, target_s, runs=5):
+    """The two-engram chain restated in torch-CPU ops: both engrams' hash_ids on all tokens, then
+    lookup + inject of the first and of the second on its output for a token sample (inject is
+    per token, so a sample is the chain on those tokens); per-token times added."""
+    threads = cpu_threads()
+    ces = [CpuEngram(e) for e in engs]
+    ids_c, pos_c = ids.cpu(), pos.cpu()
+    h_all = hidden.reshape(-1, hidden.shape[-1]).cpu()
+    T = h_all.shape[0]
+    idx = {}
+
+    def hash_both():
+        idx[0] = ces[0].hash_ids(ids_c, pos_c).reshape(len(ces[0].tables), -1)
+        idx[1] = ces[1].hash_ids(ids_c, pos_c).reshape(len(ces[1].tables), -1)
+
+    hash_s_per_tok = median_s(hash_both, runs) / T
+
+    def chain(sample):
+        out = ces[0].inject(h_all[sample], idx[0][:, sample])
+        return ces[1].inject(out, idx[1][:, sample])
+
+    rng = np.random.Generator(np.random.PCG64(1))
+    probe = torch.from_numpy(np.sort(rng.choice(T, 64, replace=False)))
+    chain(probe)
+    t0 = time.perf_counter()
+    chain(probe)
+    per_tok = (time.perf_counter() - t0) / probe.numel()
+    n = int(min(T, max(64, target_s / max(per_tok, 1e-9) / (runs + 1))))
+    sample = torch.from_numpy(np.sort(rng.choice(T, n, replace=False)))
+    per_tok = median_s(lambda: chain(sample), runs) / n + hash_s_per_tok
+    return _baseline(1.0 / per_tok, "tokens/s", threads,
+                     f"both engrams' hash_ids on all {T} tokens, then the two lookups + injects "
+                     f"chained on {n} of them; each the median of {runs} runs after 1 warm-up; "
+                     f"per-token times added")
+
+
+def cpu_baseline_update(ce, keys, grads, offsets, runs=5):
+    """The sparse update of one batch restated in torch-CPU ops: torch.unique + index_add_ of the
+    lookups' gradient rows (rows.py:81, 117-118), then each table's lazy row-wise Adam step with
+    stochastic bf16 rounding on its touched rows (optim.py:65-133, noise from torch.randint as
+    optim.py:40 draws it). Runs on (and updates) the host copy of the tables."""
+    oracle = _oracle()
+    threads = cpu_threads()
+    keys, grads = keys.cpu(), grads.cpu()
+    D = grads.shape[1]
+    m = [torch.zeros_like(t) for t in ce.tables]
+    v = [torch.zeros(t.shape[0], dtype=torch.float32) for t in ce.tables]
+    offs = torch.tensor(offsets, dtype=torch.int64)
+    noise = lambda rows, which: torch.randint(0, 1 << 16, (rows.numel(), D), dtype=torch.int32)
+
+    def update():
+        uniq, _inv, acc = oracle.dedup_torch(keys, grads)
+        b = torch.searchsorted(uniq, offs).tolist()
+        for k, table in enumerate(ce.tables):
+            oracle.sparse_adam_step(table, m[k], v[k], uniq[b[k]:b[k + 1]] - offsets[k],
+                                    acc[b[k]:b[k + 1]], 1, 5e-3, noise=noise)
+
+    sec = median_s(update, runs)
+    n = keys.numel()
+    return _baseline(n / sec, "lookups/s", threads,
+                     f"dedup + row-wise Adam (SR) of all {n} lookups of one batch; median of {runs} "
+                     f"runs after 1 warm-up", ms_per_update=sec * 1e3)
 
 
 SETTLE_S = 0.25  # sustained replays before a timed one (the part's clock settles in ~0.1-0.2 s)
@@ -308,7 +481,7 @@ def graph_step_ms(step, n_steps):
     return wall / n_steps * 1e3
 
 
-def measure_tiny(dev, steps=32, cycle=4):
+def measure_tiny(dev, steps=32, cycle=4, cpu=False):
     """The tiny fp32 forward: one engram, orders {2,3}, 16 tables of 65,536 x 64 fp32, hidden
     1024 fp32, one document of 2048 uniform ids over 32,000; `cycle` distinct seeded batches.
     Forward tokens/s, the gather's HBM roofline and the projection's fp32 MFMA roofline."""
@@ -343,12 +516,16 @@ def measure_tiny(dev, steps=32, cycle=4):
                  "achieved_tflops": flop / (gate_ms * 1e-3) / 1e12, "peak_tflops": F32_PEAK_TFLOPS,
                  "frac": flop / (gate_ms * 1e-3) / 1e12 / F32_PEAK_TFLOPS},
     }
+    if cpu:
+        with torch.inference_mode():
+            out["cpu_baseline"] = cpu_baseline_tiny(eng, batches[0])
+        out["cpu_baseline"]["gpu_value"] = out["tokens_per_s"]
     del eng, batches, mems
     torch.cuda.empty_cache()
     return out
 
 
-def measure_two_engram(dev, steps=3):
+def measure_two_engram(dev, steps=3, cpu=False, cpu_seconds=10.0):
     """Two Gemma-scale engrams (layers 0 and 29: seeds 0 and 290,203) with a canon map merging
     15 % of the ids, prefill batch 8 x 8192 packed Zipf tokens, hidden 5376 bf16: the hidden
     state through the first engram, then the second. Forward tokens/s of the chain and the
@@ -385,6 +562,10 @@ def measure_two_engram(dev, steps=3):
                    "achieved_gbs": gbytes / (gather_ms * 1e-3) / 1e9,
                    "frac": gbytes / (gather_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
+    if cpu:
+        with torch.inference_mode():
+            out["cpu_baseline"] = cpu_baseline_two_engram(engs, ids, pos, hidden, cpu_seconds)
+        out["cpu_baseline"]["gpu_value"] = out["tokens_per_s"]
     del engs, hidden, state
     torch.cuda.empty_cache()
     return out
@@ -467,6 +648,7 @@ def main():
 
         decode_ms = replay_ms([(lambda k=k: decode(k)) for k in range(CYCLE)], 2)
         decode_tokens = dsteps[0][0].shape[0]
+        decode_cpu_input = dsteps[0]
         del dsteps
 
         # A plain device copy of the gather's output size (each launch on other buffers, as the
@@ -477,6 +659,20 @@ def main():
         views = [(ring[2 * k * gbytes_out:(2 * k + 1) * gbytes_out],
                   ring[(2 * k + 1) * gbytes_out:(2 * k + 2) * gbytes_out]) for k in range(CYCLE)]
         copy_same_ms = replay_ms([(lambda k=k: views[k][1].copy_(views[k][0])) for k in range(CYCLE)], 2)
+        # the same bytes through the calibration kernels: a non-temporal 16-byte copy (its two
+        # best launch shapes), and the gather's access shape -- random 128-byte rows of these
+        # tables, written concatenated in token order -- with row ids from integer arithmetic
+        # instead of the hash (no dependent load in front of the row reads)
+        calib = calib_lib()
+        sid = lambda: ops.stream_of(dev)  # the capturing stream, read at each call
+        copy_nt_ms = min(replay_ms([(lambda k=k: calib_ok(calib.me_calib_copy_nt(
+            views[k][0].data_ptr(), views[k][1].data_ptr(), gbytes_out, u, sid()))) for k in range(CYCLE)], 2)
+            for u in (3, 12))
+        tptrs = (ctypes.c_void_p * len(eng.tables))(*[t.weight.data_ptr() for t in eng.tables])
+        trows = (ctypes.c_int64 * len(eng.tables))(*eng.table_rows)
+        random_rows_ms = replay_ms([(lambda k=k: calib_ok(calib.me_calib_random_rows(
+            tptrs, trows, len(eng.tables), views[k][1].data_ptr(), T, 77 * k + 1, sid())))
+            for k in range(CYCLE)], 2)
         del views, ring
 
         # The sparse update (dedup + row-wise Adam with stochastic rounding) of the same
@@ -506,10 +702,12 @@ def main():
         adam_ms = replay_ms([(lambda k=k: adam(k)) for k in range(CYCLE)], 2)
         n_lookups = ubatches[0][0].numel()
         n_uniq = float(np.mean([u[4] for u in ubatches]))
+        update_cpu_input = (ubatches[0][0].cpu(), ubatches[0][1].cpu())
         del ubatches, exp_avgs, exp_avg_sqs
     train_ms = training_step_ms(dev, batches, steps=30, warmup=10)
-    tiny = measure_tiny(dev)
-    two = measure_two_engram(dev)
+    cpu = not args.no_cpu_baseline
+    tiny = measure_tiny(dev, cpu=cpu)
+    two = measure_two_engram(dev, cpu=cpu, cpu_seconds=args.cpu_seconds)
     with torch.inference_mode():
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -568,6 +766,11 @@ def main():
             "copy_1gib_gbs": copy_gbs,
             "copy_same_size_ms": copy_same_ms,
             "copy_same_size_gbs": 2.0 * gbytes_out / (copy_same_ms * 1e-3) / 1e9,
+            "copy_same_size_nt_ms": copy_nt_ms,
+            "copy_same_size_nt_gbs": 2.0 * gbytes_out / (copy_nt_ms * 1e-3) / 1e9,
+            "random_rows_same_size_ms": random_rows_ms,
+            "random_rows_same_size_gbs": 2.0 * gbytes_out / (random_rows_ms * 1e-3) / 1e9,
+            "gather_over_random_rows": random_rows_ms / gather_ms,
         },
         "roofline_gate": {
             "kernel": "K/V projection + gate + residual (gate224_kernel key + value passes on 256 x 224 "
@@ -621,10 +824,23 @@ def main():
                   "durations: per-kernel graph replays over the 16 batches between HIP events",
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
+    if cpu:
         ids, pos, hidden = batches[0]
         with torch.inference_mode():
-            result["cpu_baseline"] = cpu_baseline(eng, ids, pos, hidden, args.cpu_seconds)
+            ce = CpuEngram(eng)
+            result["cpu_baseline"] = cpu_baseline(eng, ids, pos, hidden, args.cpu_seconds, cpu_eng=ce)
+            # the other configurations' CPU restatements, each beside the GPU figure in its unit
+            dec = cpu_baseline_decode(ce, *decode_cpu_input)
+            dec["gpu_value"] = decode_tokens / (decode_ms * 1e-3)
+            upd = cpu_baseline_update(ce, *update_cpu_input, key_bound_offsets(eng))
+            upd["gpu_value"] = n_lookups / ((keys_ms + sums_ms + adam_ms) * 1e-3)
+            del ce
+        result["cpu_baseline_configs"] = {
+            "tiny_forward": tiny.pop("cpu_baseline"),
+            "serving_decode": dec,
+            "two_engram_canon": two.pop("cpu_baseline"),
+            "sparse_update": upd,
+        }
     print(json.dumps(result), flush=True)
 
 

@@ -15,6 +15,10 @@ CSRC = os.path.join(PKG, "csrc")
 OBJ_DIR = os.path.join(CSRC, "_build")
 LIB_NAME = "libmicro_engram_amd.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
+# calibration kernels of the benchmark (csrc/calib/*.hip): a library of their own, loaded by
+# bench.py only
+CALIB_DIR = os.path.join(CSRC, "calib")
+CALIB_LIB_PATH = os.path.join(PKG, "libmicro_engram_calib.so")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -41,7 +45,8 @@ def sources():
 
 
 def _compile(src):
-    obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
+    sub = "calib_" if os.path.dirname(src) == CALIB_DIR else ""
+    obj = os.path.join(OBJ_DIR, sub + os.path.basename(src)[:-4] + ".o")
     cmd = [_hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -49,21 +54,34 @@ def _compile(src):
     return obj
 
 
-def build(verbose=False, jobs=None):
-    """Compile every kernel source and link the library. Returns the library path."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
-    with ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIB_PATH + ".tmp"
+def calib_sources():
+    return sorted(os.path.join(CALIB_DIR, f) for f in os.listdir(CALIB_DIR) if f.endswith(".hip"))
+
+
+def _link(objs, path):
+    tmp = path + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"[micro_engram] linking {LIB_NAME} failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"[micro_engram] linking {os.path.basename(path)} failed:\n{res.stdout}\n"
+                           f"{res.stderr}")
+    os.replace(tmp, path)
+
+
+def build(verbose=False, jobs=None):
+    """Compile every kernel source and link the library (and the benchmark's calibration
+    library). Returns the library path."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    srcs = sources()
+    calib = calib_sources()
+    jobs = jobs or min(len(srcs) + len(calib), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(_compile, srcs + calib))
+    _link(objs[:len(srcs)], LIB_PATH)
+    _link(objs[len(srcs):], CALIB_LIB_PATH)
     if verbose:
-        print(f"[micro_engram] built {LIB_PATH} from {len(srcs)} sources")
+        print(f"[micro_engram] built {LIB_PATH} from {len(srcs)} sources, "
+              f"{os.path.basename(CALIB_LIB_PATH)} from {len(calib)}")
     return LIB_PATH
 
 
