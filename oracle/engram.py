@@ -260,7 +260,7 @@ def inject(hidden, mem, w_key, w_value, gate="scalar_sqrt", q_scale_delta=None, 
 
 
 def inject_backward(grad_out, hidden, mem, w_key, w_value, gate="scalar_sqrt", q_scale_delta=None,
-                    k_scale_delta=None, keep=None):
+                    k_scale_delta=None, keep=None, stats=None, with_terms=False):
     """Closed-form gradients of inject (module.py:239-261) in float64, from the gradient of its
     output: (d hidden, d K, d V, d q_scale_delta, d k_scale_delta), with K = W_K mem and V = W_V
     mem the key / value Linear outputs (their weight and mem gradients are the plain products
@@ -272,7 +272,17 @@ def inject_backward(grad_out, hidden, mem, w_key, w_value, gate="scalar_sqrt", q
       ds0 = ds / (2 sqrt|s0|) if |s0| >= 1e-6 else 0 (scalar_sqrt; the scalar gate: ds0 = ds)
       a = ds0 r_h r_k / sqrt(d)
       d hidden = g + a (w K - x r_h^2 sck / d);  dK = a (w x - K r_k^2 sck / d)
-      d q_scale_j = ks_j sum_tokens a x_j K_j;  d k_scale_j = qs_j sum_tokens a x_j K_j"""
+      d q_scale_j = ks_j sum_tokens a x_j K_j;  d k_scale_j = qs_j sum_tokens a x_j K_j
+
+    stats: optional [N, 4] (sum x^2, sum K^2, sck, alpha) of a forward that ran elsewhere (the GPU
+    forward's row statistics): r_h, r_k, s0 and alpha then come from them instead of from x, K,
+    so the closed form is evaluated at that forward's point -- near s0 = 0 the gradient's
+    1 / sqrt|s0| factor otherwise turns the forward's own fp32 rounding of s0 into large
+    differences. with_terms: also return the scale of each gradient's rounding errors: per
+    element the magnitudes its products are made of (|a w K| + |a x r_h^2 sck / d| for d hidden,
+    |a w x| + |a K r_k^2 sck / d| for dK, sum_tokens of |a x K| for the scale gradients), each
+    token's |a| taken times (1 + sum |g V| / |d alpha|): d alpha is a sum of g V over the row,
+    whose rounding is relative to sum |g V|, not to its own (possibly cancelled) size."""
     f = lambda t: t.detach().double()
     x, e, g = f(hidden), f(mem), f(grad_out)
     d = x.shape[-1]
@@ -283,12 +293,16 @@ def inject_backward(grad_out, hidden, mem, w_key, w_value, gate="scalar_sqrt", q
     else:
         qs = ks = torch.ones(d, dtype=torch.float64)
     w = qs * ks
-    rh = 1.0 / torch.sqrt((x * x).mean(-1) + eps)
-    rk = 1.0 / torch.sqrt((K * K).mean(-1) + eps)
-    sck = (x * w * K).sum(-1)
+    if stats is None:
+        sx2, sk2, sck = (x * x).sum(-1), (K * K).sum(-1), (x * w * K).sum(-1)
+    else:
+        st = f(stats)
+        sx2, sk2, sck = st[:, 0], st[:, 1], st[:, 2]
+    rh = 1.0 / torch.sqrt(sx2 / d + eps)
+    rk = 1.0 / torch.sqrt(sk2 / d + eps)
     s0 = rh * rk * sck / d ** 0.5
     s = s0.sign() * s0.abs().clamp_min(1e-6).sqrt() if gate == "scalar_sqrt" else s0
-    alpha = torch.sigmoid(s)
+    alpha = torch.sigmoid(s) if stats is None else f(stats)[:, 3]
     kf = torch.ones_like(alpha) if keep is None else f(keep.reshape(-1).to(torch.float64))
     dV = (alpha * kf)[:, None] * g
     dalpha = kf * (g * V).sum(-1)
@@ -298,10 +312,18 @@ def inject_backward(grad_out, hidden, mem, w_key, w_value, gate="scalar_sqrt", q
     else:
         ds0 = ds
     a = ds0 * rh * rk / d ** 0.5
-    dx = g + a[:, None] * (w * K - x * (rh * rh * sck / d)[:, None])
-    dK = a[:, None] * (w * x - K * (rk * rk * sck / d)[:, None])
+    c2, c3 = (rh * rh * sck / d)[:, None], (rk * rk * sck / d)[:, None]
+    dx = g + a[:, None] * (w * K - x * c2)
+    dK = a[:, None] * (w * x - K * c3)
     P = (a[:, None] * x * K).sum(0)
-    return dx, dK, dV, ks * P, qs * P
+    if not with_terms:
+        return dx, dK, dV, ks * P, qs * P
+    gv = kf * (g * V).abs().sum(-1)
+    cond = torch.where(dalpha != 0, 1 + gv / dalpha.abs().clamp_min(1e-300), torch.ones_like(gv))
+    aa = (a.abs() * cond)[:, None]
+    terms = (aa * ((w * K).abs() + (x * c2).abs()), aa * ((w * x).abs() + (K * c3).abs()),
+             (aa * (x * K).abs()).sum(0))
+    return dx, dK, dV, ks * P, qs * P, terms
 
 
 # ------------------------------------------------------------------------------------- dedup

@@ -271,3 +271,86 @@ def test_empty_batch_zeroes_the_scale_gradients_in_a_graph():
         graph.replay()
         torch.cuda.synchronize()
         assert not gq.any() and not gk.any()
+
+
+def _ulp_bf16(x):
+    x = x.abs().clamp_min(2.0 ** -126)
+    return torch.pow(2.0, torch.floor(torch.log2(x)) - 7)
+
+
+def _check_backward_at_forward_stats(eng, x, mem, g, dtype, rows=None, keep=None):
+    """The HIP gate backward against the float64 closed form evaluated at the GPU forward's own
+    row statistics (oracle.inject_backward(stats=...)), on every token in `rows` (all by
+    default) -- including those with scalar_sqrt scores near 0, whose gradients the end-to-end
+    tests leave out. Per element: |gpu - ref| <= rounding of the stored value + a multiple of
+    the magnitudes the products are made of (bf16: K and V are bf16-rounded on the GPU)."""
+    from micro_engram_fork_amd import ops
+    from micro_engram_fork_amd._lib import ME_GATE_SCALAR_SQRT
+
+    wk, wv = eng.key.weight.detach(), eng.value.weight.detach()
+    dq, dk = eng.q_scale.detach(), eng.k_scale.detach()
+    out, alpha, stats = ops.gate_residual(x, mem, wk, wv, dq, dk, ME_GATE_SCALAR_SQRT, keep, True, True)
+    gh, gK, gV, gq, gk = ops.gate_backward(g, x, mem, wk, wv, dq, dk, ME_GATE_SCALAR_SQRT, keep, stats)
+    sel = torch.arange(x.shape[0]) if rows is None else rows
+    c = lambda t: t.detach().cpu()[sel]
+    ref = oracle.inject_backward(c(g), c(x), c(mem), wk.cpu(), wv.cpu(), "scalar_sqrt", dq.cpu(),
+                                 dk.cpu(), keep=None if keep is None else c(keep), stats=c(stats),
+                                 with_terms=True)
+    t_dx, t_dk, t_p = ref[5]
+    rel = 2.0 ** -6 if dtype == torch.bfloat16 else 1e-5
+    store = _ulp_bf16 if dtype == torch.bfloat16 else (lambda v: 1e-6 * v.abs())
+    for name, got, want, term in (("hidden", gh, ref[0], t_dx), ("dK", gK, ref[1], t_dk),
+                                  ("dV", gV, ref[2], torch.zeros_like(ref[2]))):
+        got = got.detach().cpu()[sel].double()
+        bound = store(want) + rel * term + 1e-30
+        bad = (got - want).abs() > bound
+        assert not bool(bad.any()), (name, int(bad.sum()), float((got - want).abs().max()))
+    if rows is None:  # the scale gradients sum over every token
+        ks, qs = 1 + dk.cpu().double(), 1 + dq.cpu().double()
+        for name, got, want, scale in (("q_scale", gq, ref[3], ks), ("k_scale", gk, ref[4], qs)):
+            err = (got.detach().cpu().double() - want).abs()
+            assert bool((err <= 4 * rel * scale.abs() * t_p + 1e-12).all()), (name, float(err.max()))
+    s = torch.log(alpha / (1 - alpha)).cpu()[sel]
+    return int((s.abs() < 0.1).sum())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,d,dim,heads", [(300, 264, 8, 3), (1000, 520, 16, 4)])
+def test_backward_at_the_forwards_stats_on_every_token(dtype, n, d, dim, heads):
+    # no output gradient is zeroed: tokens with |s| < 0.1 are compared like the others
+    torch.manual_seed(n + d + 1)
+    eng = _make(dtype, "scalar_sqrt", d, dim, heads)
+    ids = torch.randint(0, 1000, (1, n), device=DEV)
+    x = (torch.randn(n, d) * 3).to(dtype).to(DEV)
+    g = torch.randn(n, d).to(dtype).to(DEV)
+    keep = torch.rand(n, device=DEV) > 0.2
+    mem = eng.hashed_memory(ids)
+    near_zero = _check_backward_at_forward_stats(eng, x, mem, g, dtype, keep=keep)
+    _check_backward_at_forward_stats(eng, x, mem, g, dtype)
+    if n >= 1000:
+        assert near_zero > 0  # the case the end-to-end tests leave out is covered
+
+
+def test_backward_at_the_forwards_stats_gemma_prefill():
+    # the headline shape (8192 tokens, model dim 5376, 24 bf16 tables): every token with
+    # |s| < 0.1 plus 256 others, against the float64 closed form at the GPU forward's stats
+    eng = synthetic.build_engram("gemma", DEV, seed=7)
+    ids, pos, hidden = synthetic.prefill_inputs(seed=5, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    x = hidden.reshape(-1, hidden.shape[-1])
+    g = torch.randn(x.shape, generator=gen, device=DEV).to(torch.bfloat16)
+    mem = eng.hashed_memory(ids, pos)
+    from micro_engram_fork_amd import ops
+    from micro_engram_fork_amd._lib import ME_GATE_SCALAR_SQRT
+
+    _, alpha = ops.gate_residual(x, mem, eng.key.weight.detach(), eng.value.weight.detach(),
+                                 eng.q_scale.detach(), eng.k_scale.detach(), ME_GATE_SCALAR_SQRT,
+                                 None, True)
+    s = torch.log(alpha / (1 - alpha)).cpu()
+    low = torch.nonzero(s.abs() < 0.1).reshape(-1)
+    others = torch.randperm(x.shape[0], generator=torch.Generator().manual_seed(3))[:256]
+    rows = torch.unique(torch.cat([low, others]))
+    near_zero = _check_backward_at_forward_stats(eng, x, mem, g, torch.bfloat16, rows=rows)
+    assert near_zero == low.numel() > 0
+    del eng
+    torch.cuda.empty_cache()
