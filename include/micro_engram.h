@@ -215,8 +215,9 @@ int me_kv_proj(const void *mem, int64_t n, int64_t mem_dim, const void *w_key, c
  *
  *   hidden, out   [n, model_dim] of hidden_dtype (out may equal hidden)
  *   k_proj, v_proj  rows of K and V (dtype), kv_stride elements apart (e.g. the two halves of
- *                 one [n, 2 model_dim] GEMM output); model_dim and kv_stride multiples of 8, every
- *                 tensor 16-byte aligned
+ *                 one [n, 2 model_dim] GEMM output); any model_dim >= 1 and kv_stride >=
+ *                 model_dim (16-byte accesses when both are multiples of 8 and every tensor is
+ *                 16-byte aligned, element accesses otherwise: an engram of any model dim)
  *   q/k_scale_delta, keep, alpha_out, row_stats   as for me_gate_residual
  */
 int me_gate_rows(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
@@ -224,6 +225,38 @@ int me_gate_rows(const void *hidden, int hidden_dtype, int64_t n, int64_t model_
                  const void *q_scale_delta, const void *k_scale_delta, int scale_dtype,
                  int gate_mode, const uint8_t *keep, void *out, float *alpha_out,
                  float *row_stats, void *stream);
+
+/*
+ * me_gate_rows_backward_workspace_size -- bytes of workspace me_gate_rows_backward needs.
+ */
+int me_gate_rows_backward_workspace_size(int64_t n, int64_t model_dim, size_t *bytes);
+
+/*
+ * me_gate_rows_backward -- gradients of me_gate_rows from the same K and V rows: what autograd
+ * computes through MicroEngram.inject after its two nn.Linear calls (micro_engram/module.py:
+ * 239-261), the arithmetic of me_gate_backward (which recomputes K and V on MFMA tiles, for the
+ * shapes those take) for any model dim:
+ *
+ *   dV = round(alpha keep g);  d alpha = keep sum g V;  ds = d alpha alpha (1 - alpha)
+ *   ds0 = ds / (2 sqrt|s0|) where |s0| >= 1e-6, else 0 (ME_GATE_SCALAR_SQRT); ds (ME_GATE_SCALAR)
+ *   a = ds0 r_h r_k / sqrt(d); d hidden = g + round(a w K - a r_h^2 sck / d x)
+ *   dK = round(a w x - a r_k^2 sck / d K);  d q_scale_delta_j = ks_j P_j, d k_scale_delta_j = qs_j P_j
+ *   with w = qs ks, P_j = sum over tokens of a x_j K_j
+ *
+ *   hidden, grad_out, grad_hidden   [n, model_dim] of hidden_dtype
+ *   k_proj, v_proj  the forward's K and V rows (dtype), kv_stride elements apart
+ *   row_stats     [n, 4] fp32 of the forward (me_gate_rows or me_gate_residual on the same K, V)
+ *   grad_key, grad_value   [n, model_dim] of dtype: the gradients of the Linear outputs K and V
+ *   grad_q_scale, grad_k_scale   [model_dim] fp32 (ME_GATE_SCALAR_SQRT only)
+ *   workspace     at least me_gate_rows_backward_workspace_size(n, model_dim) bytes
+ */
+int me_gate_rows_backward(const void *hidden, int hidden_dtype, int64_t n, int64_t model_dim,
+                          const void *k_proj, const void *v_proj, int64_t kv_stride, int dtype,
+                          const void *q_scale_delta, const void *k_scale_delta, int scale_dtype,
+                          int gate_mode, const uint8_t *keep, const void *grad_out,
+                          const float *row_stats, void *grad_hidden, void *grad_key,
+                          void *grad_value, float *grad_q_scale, float *grad_k_scale,
+                          void *workspace, size_t workspace_size, void *stream);
 
 /*
  * me_gate_backward_workspace_size -- bytes of workspace me_gate_backward needs.

@@ -36,6 +36,10 @@ SIGNATURES = {
     "me_kv_proj": [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr],
     "me_gate_rows": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr, c_int,
                      c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr],
+    "me_gate_rows_backward_workspace_size": [c_i64, c_i64, ctypes.POINTER(c_size)],
+    "me_gate_rows_backward": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_int, c_ptr, c_ptr,
+                              c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+                              c_ptr, c_size, c_ptr],
     "me_gate_backward_workspace_size": [c_i64, c_i64, ctypes.POINTER(c_size)],
     "me_gate_backward": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_int,
                          c_ptr, c_ptr, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,

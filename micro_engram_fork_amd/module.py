@@ -23,6 +23,7 @@ Differences from the reference, all deliberate:
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import ops
 from ._lib import ME_GATE_SCALAR, ME_GATE_SCALAR_SQRT, ME_MAX_ORDER, ME_MAX_TABLES
@@ -75,6 +76,43 @@ class _GateResidual(torch.autograd.Function):
         wk, wv = w_key.detach(), w_value.detach()
         g_hidden, g_key, g_value, g_q, g_k = ops.gate_backward(
             grad_out.contiguous(), hidden.detach(), mem.detach(), wk, wv,
+            None if q_delta is None else q_delta.detach(),
+            None if k_delta is None else k_delta.detach(), ctx.gate_mode, keep, stats)
+        m = mem.detach().reshape(g_key.shape[0], -1)
+        d_mem = torch.addmm(g_key @ wk, g_value, wv).reshape(mem.shape) if need[1] else None
+        d_wk = g_key.t() @ m if need[2] else None
+        d_wv = g_value.t() @ m if need[3] else None
+        d_q = g_q.to(q_delta.dtype) if need[4] else None
+        d_k = g_k.to(k_delta.dtype) if need[5] else None
+        return g_hidden if need[0] else None, d_mem, d_wk, d_wv, d_q, d_k, None, None
+
+
+class _GateResidualRows(torch.autograd.Function):
+    """The same as _GateResidual for shapes the MFMA kernels do not take (model dim not a
+    multiple of 8, memory rows not a multiple of 16 bytes): the key / value projections are the
+    library GEMM of nn.Linear (module.py:245, 254), the gate, residual add and their backward the
+    HIP row kernels (me_gate_rows, me_gate_rows_backward); K and V are kept for the backward."""
+
+    @staticmethod
+    def forward(ctx, hidden, mem, w_key, w_value, q_delta, k_delta, gate_mode, keep):
+        m = mem.reshape(-1, mem.shape[-1])
+        k = torch.nn.functional.linear(m, w_key.detach())
+        v = torch.nn.functional.linear(m, w_value.detach())
+        q = None if q_delta is None else q_delta.detach()
+        kd = None if k_delta is None else k_delta.detach()
+        out, alpha, stats = ops.gate_rows(hidden, k, v, q, kd, gate_mode, keep, True, True)
+        ctx.save_for_backward(hidden, mem, w_key, w_value, q_delta, k_delta, keep, stats, k, v)
+        ctx.gate_mode = gate_mode
+        ctx.mark_non_differentiable(alpha)
+        return out, alpha
+
+    @staticmethod
+    def backward(ctx, grad_out, _grad_alpha):
+        hidden, mem, w_key, w_value, q_delta, k_delta, keep, stats, k, v = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        wk, wv = w_key.detach(), w_value.detach()
+        g_hidden, g_key, g_value, g_q, g_k = ops.gate_rows_backward(
+            grad_out.contiguous(), hidden.detach(), k, v,
             None if q_delta is None else q_delta.detach(),
             None if k_delta is None else k_delta.detach(), ctx.gate_mode, keep, stats)
         m = mem.detach().reshape(g_key.shape[0], -1)
@@ -337,15 +375,25 @@ class MicroEngram(nn.Module):
             mem = mem.to(reader.dtype)  # rows stored in another dtype (module.py:234-238)
         sqrt = self.gate == "scalar_sqrt"
         mode = ME_GATE_SCALAR_SQRT if sqrt else ME_GATE_SCALAR
+        fits = ops.fits_mfma(hidden.shape[-1], mem.shape[-1], mem.dtype)
         if self._needs_grad(hidden) or mem.requires_grad:
-            out, alpha = _GateResidual.apply(hidden, mem, self.key.weight, self.value.weight,
-                                             self.q_scale if sqrt else None,
-                                             self.k_scale if sqrt else None, mode, keep)
+            fn = _GateResidual if fits else _GateResidualRows
+            out, alpha = fn.apply(hidden, mem, self.key.weight, self.value.weight,
+                                  self.q_scale if sqrt else None, self.k_scale if sqrt else None,
+                                  mode, keep)
             if self.training:
                 self._record_gate(alpha)
             return out
         q = self.q_scale.detach() if sqrt else None
         k = self.k_scale.detach() if sqrt else None
+        if not fits:  # any width: library GEMMs for K and V, then the row kernel
+            m = mem.reshape(-1, mem.shape[-1])
+            outs = ops.gate_rows(hidden, F.linear(m, self.key.weight.detach()),
+                                 F.linear(m, self.value.weight.detach()), q, k, mode, keep,
+                                 self.training)
+            if self.training:
+                self._record_gate(outs[1])
+            return outs[0]
         n_tok = hidden.numel() // hidden.shape[-1]
         if mem.dtype == torch.bfloat16:
             limit = self.few_tokens_max

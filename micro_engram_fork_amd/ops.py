@@ -392,6 +392,128 @@ def _(mem, w_key, w_value):
     return mem.new_empty((mem.shape[0], 2 * w_key.shape[0]))
 
 
+def fits_mfma(model_dim, mem_dim, dtype):
+    """Whether the MFMA gate kernels (me_gate_residual, me_gate_backward, me_kv_proj) take this
+    shape: model dim a multiple of 8 and memory rows a multiple of 16 bytes. Other shapes run
+    the row kernels (me_gate_rows, me_gate_rows_backward) after library GEMMs."""
+    esize = 2 if dtype == torch.bfloat16 else 4
+    return model_dim % 8 == 0 and (mem_dim * esize) % 16 == 0
+
+
+def _kv_rows(k, v, d):
+    """K and V rows for the row kernels: one stride for both (contiguous [N, d] tensors)."""
+    k, v = k.reshape(-1, d).contiguous(), v.reshape(-1, d).contiguous()
+    if k.dtype != v.dtype:
+        raise ValueError("[micro_engram] K and V rows must share one dtype")
+    return k, v
+
+
+@_custom_op("gate_rows")
+def gate_rows(hidden: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+              q_scale_delta: Optional[torch.Tensor], k_scale_delta: Optional[torch.Tensor],
+              gate_mode: int, keep: Optional[torch.Tensor], with_alpha: bool,
+              with_stats: bool = False) -> List[torch.Tensor]:
+    """The gate and residual add (module.py:239-261) from the key / value Linear outputs K, V
+    [N, d] computed elsewhere: me_gate_rows, any model dim. [out] (+ alpha, + row stats)."""
+    dev = require_gpu(hidden, k, v, q_scale_delta, k_scale_delta, keep)
+    d = hidden.shape[-1]
+    x = hidden.reshape(-1, d).contiguous()
+    N = x.shape[0]
+    k, v = _kv_rows(k, v, d)
+    if k.shape[0] != N:
+        raise ValueError(f"[micro_engram] K/V rows {tuple(k.shape)} do not match {N} tokens")
+    q_scale_delta, k_scale_delta, scale_code = _scales(q_scale_delta, k_scale_delta, gate_mode)
+    keep_u8 = _keep_u8(keep, N)
+    out = torch.empty_like(x)
+    alpha = torch.empty(N, dtype=torch.float32, device=dev) if with_alpha else None
+    stats = torch.empty((N, 4), dtype=torch.float32, device=dev) if with_stats else None
+    call("me_gate_rows", x.data_ptr(), dtype_code(x), N, d, k.data_ptr(), v.data_ptr(), d,
+         dtype_code(k), _p(q_scale_delta), _p(k_scale_delta), scale_code, gate_mode, _p(keep_u8),
+         out.data_ptr(), _p(alpha), _p(stats), stream_of(dev))
+    res = [out.reshape(hidden.shape)]
+    if with_alpha:
+        res.append(alpha)
+    if with_stats:
+        res.append(stats)
+    return res
+
+
+@gate_rows.register_fake
+def _(hidden, k, v, q_scale_delta, k_scale_delta, gate_mode, keep, with_alpha, with_stats=False):
+    n = hidden.numel() // hidden.shape[-1]
+    res = [torch.empty_like(hidden)]
+    if with_alpha:
+        res.append(hidden.new_empty((n,), dtype=torch.float32))
+    if with_stats:
+        res.append(hidden.new_empty((n, 4), dtype=torch.float32))
+    return res
+
+
+@_custom_op("gate_rows_backward")
+def gate_rows_backward(grad_out: torch.Tensor, hidden: torch.Tensor, k: torch.Tensor,
+                       v: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
+                       k_scale_delta: Optional[torch.Tensor], gate_mode: int,
+                       keep: Optional[torch.Tensor], stats: torch.Tensor) -> List[torch.Tensor]:
+    """Gradients of gate_rows from the same K, V rows (me_gate_rows_backward, any model dim):
+    [grad_hidden, grad of K [N, d], grad of V [N, d], grad_q_scale_delta, grad_k_scale_delta
+    ([d] fp32; empty for the scalar gate)]."""
+    dev = require_gpu(grad_out, hidden, k, v, q_scale_delta, k_scale_delta, keep, stats)
+    d = hidden.shape[-1]
+    x = hidden.reshape(-1, d).contiguous()
+    N = x.shape[0]
+    k, v = _kv_rows(k, v, d)
+    g = grad_out.reshape(-1, d).to(x.dtype).contiguous()
+    stats = stats.contiguous()
+    if tuple(stats.shape) != (N, 4) or stats.dtype != torch.float32:
+        raise ValueError(f"[micro_engram] stats must be fp32 [{N}, 4], got {tuple(stats.shape)}")
+    q_scale_delta, k_scale_delta, scale_code = _scales(q_scale_delta, k_scale_delta, gate_mode)
+    keep_u8 = _keep_u8(keep, N)
+    grad_hidden = torch.empty_like(x)
+    grad_k = torch.empty((N, d), dtype=k.dtype, device=dev)
+    grad_v = torch.empty((N, d), dtype=k.dtype, device=dev)
+    sqrt = gate_mode == _lib.ME_GATE_SCALAR_SQRT
+    grad_q = torch.empty(d if sqrt else 0, dtype=torch.float32, device=dev)
+    grad_kd = torch.empty(d if sqrt else 0, dtype=torch.float32, device=dev)
+    size = ctypes.c_size_t(0)
+    call("me_gate_rows_backward_workspace_size", N, d, ctypes.byref(size))
+    ws = torch.empty(max(size.value, 16), dtype=torch.uint8, device=dev)
+    call("me_gate_rows_backward", x.data_ptr(), dtype_code(x), N, d, k.data_ptr(), v.data_ptr(), d,
+         dtype_code(k), _p(q_scale_delta), _p(k_scale_delta), scale_code, gate_mode, _p(keep_u8),
+         g.data_ptr(), stats.data_ptr(), grad_hidden.data_ptr(), grad_k.data_ptr(),
+         grad_v.data_ptr(), grad_q.data_ptr() if sqrt else None, grad_kd.data_ptr() if sqrt else None,
+         ws.data_ptr(), ws.numel(), stream_of(dev))
+    return [grad_hidden.reshape(hidden.shape), grad_k, grad_v, grad_q, grad_kd]
+
+
+@gate_rows_backward.register_fake
+def _(grad_out, hidden, k, v, q_scale_delta, k_scale_delta, gate_mode, keep, stats):
+    n, d = hidden.numel() // hidden.shape[-1], hidden.shape[-1]
+    nd = d if gate_mode == _lib.ME_GATE_SCALAR_SQRT else 0
+    return [torch.empty_like(hidden), k.new_empty((n, d)), k.new_empty((n, d)),
+            hidden.new_empty((nd,), dtype=torch.float32), hidden.new_empty((nd,), dtype=torch.float32)]
+
+
+def _scales(q_scale_delta, k_scale_delta, gate_mode):
+    """(q delta, k delta, dtype code) for the row kernels; (None, None, 0) for the scalar gate."""
+    if gate_mode != _lib.ME_GATE_SCALAR_SQRT:
+        return None, None, 0
+    if q_scale_delta is None or k_scale_delta is None:
+        raise ValueError("[micro_engram] the scalar_sqrt gate needs q_scale and k_scale")
+    q, k = q_scale_delta.contiguous(), k_scale_delta.contiguous()
+    if q.dtype != k.dtype:
+        k = k.to(q.dtype)
+    return q, k, dtype_code(q)
+
+
+def _keep_u8(keep, n):
+    if keep is None:
+        return None
+    keep_u8 = keep.reshape(-1).to(torch.uint8).contiguous()
+    if keep_u8.numel() != n:
+        raise ValueError(f"[micro_engram] keep has {keep_u8.numel()} entries for {n} tokens")
+    return keep_u8
+
+
 @_custom_op("gate_residual_rows")
 def gate_residual_rows(hidden: torch.Tensor, mem: torch.Tensor, w_key: torch.Tensor,
                        w_value: torch.Tensor, q_scale_delta: Optional[torch.Tensor],
