@@ -314,6 +314,24 @@ int me_dedup(const int64_t *keys, int64_t n, int64_t key_bound, const void *grad
              void *workspace, size_t workspace_size, void *stream);
 
 /*
+ * me_dedup_table_bounds -- where each table's rows lie in the unique keys of an me_dedup_keys
+ * call over concatenated-table keys (table offset + row): the bounds rows.py:123-129 splits the
+ * unique rows and sums by, and each unique key's row in its own table (the searchsorted of the
+ * keys against the table offsets), in one launch:
+ *
+ *   local_rows[i] = uniq[i] - table_offsets[t]     t = the table of uniq[i], i < *count
+ *   info[0] = *count;  info[1 + t] = number of unique keys below table_offsets[t], t <= n_tables
+ *
+ *   uniq          [n] int64 ascending (valid up to *count); count  device int64 scalar
+ *   table_offsets n_tables + 1 host int64 values, ascending, from 0 (the last: the key bound)
+ *   local_rows    [n] int64 (entries past the count are left as they are)
+ *   info          [n_tables + 2] int64 device
+ */
+int me_dedup_table_bounds(const int64_t *uniq, int64_t n, const int64_t *count,
+                          const int64_t *table_offsets, int32_t n_tables, int64_t *local_rows,
+                          int64_t *info, void *stream);
+
+/*
  * me_dedup_plan_size -- bytes of the segment plan me_dedup_keys writes for n keys.
  */
 int me_dedup_plan_size(int64_t n, size_t *bytes);

@@ -1473,6 +1473,60 @@ extern "C" int me_dedup_keys(const int64_t *keys, int64_t n, int64_t key_bound, 
                           s);
 }
 
+// ---- table bounds of the unique keys --------------------------------------------------------
+// The unique keys are concatenated-table keys (table offset + row), ascending: thread i finds the
+// table of unique key i (the last offset <= key), writes its local row, and where the table
+// changes between keys i - 1 and i it writes the first index of every table in between; the
+// thread at the count closes the tables after the last key. info = [count, bound of table 0,
+// ..., bound of table n_tables (= count)], the slices rows.py:125-129 hands each table.
+namespace me {
+namespace {
+struct TableOffsets {
+    int64_t off[ME_MAX_TABLES + 1];
+};
+
+__device__ __forceinline__ int table_of(int64_t key, const TableOffsets &t, int nt) {
+    int lo = 0, hi = nt;  // off[lo] <= key < off[hi] for keys in range
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (t.off[mid] <= key) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(kThreads) void table_bounds_kernel(const int64_t *uniq, int64_t n,
+                                                                const int64_t *count, TableOffsets t,
+                                                                int nt, int64_t *local, int64_t *info) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t cnt = *count;
+    if (i > cnt || i > n) return;
+    const int tcur = i < cnt ? table_of(uniq[i], t, nt) : nt;
+    const int tprev = i > 0 ? table_of(uniq[i - 1], t, nt) : -1;
+    if (i < cnt) local[i] = uniq[i] - t.off[tcur];
+    for (int k = tprev + 1; k <= tcur; ++k) info[1 + k] = i;
+    if (i == 0) info[0] = cnt;
+}
+}  // namespace
+}  // namespace me
+
+extern "C" int me_dedup_table_bounds(const int64_t *uniq, int64_t n, const int64_t *count,
+                                     const int64_t *table_offsets, int32_t n_tables, int64_t *local_rows,
+                                     int64_t *info, void *stream) {
+    ME_CHECK_ARG(n >= 0 && n < (int64_t{1} << 31), "n out of range");
+    ME_CHECK_ARG(n_tables >= 1 && n_tables <= ME_MAX_TABLES, "n_tables must be in [1, %d]", ME_MAX_TABLES);
+    ME_CHECK_ARG(count && table_offsets && info && (n == 0 || (uniq && local_rows)), "null pointer");
+    TableOffsets t{};
+    for (int k = 0; k <= n_tables; ++k) {
+        t.off[k] = table_offsets[k];
+        ME_CHECK_ARG(k == 0 || t.off[k] >= t.off[k - 1], "table offsets must be ascending");
+    }
+    ME_CHECK_ARG(t.off[0] == 0, "the first table offset must be 0");
+    const dim3 grid(static_cast<unsigned>(ceil_div(n + 1, kThreads)));
+    hipLaunchKernelGGL(table_bounds_kernel, grid, dim3(kThreads), 0, as_stream(stream), uniq, n, count, t,
+                       n_tables, local_rows, info);
+    return check_launch("me_dedup_table_bounds");
+}
+
 extern "C" int me_dedup_sums(const void *plan, size_t plan_size, int64_t n, const int64_t *count,
                              const void *grads, int grad_dtype, int32_t dim, float *gsum, void *stream) {
     ME_CHECK_ARG(n >= 0 && n < (int64_t{1} << 31), "n out of range");

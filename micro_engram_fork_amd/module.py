@@ -52,6 +52,26 @@ def _row_range(n_rows, rank, world):
     return start, max(0, min(per, n_rows - start))
 
 
+class _RowIds(list):
+    """The per-table row ids hash_ids / hash_prev return (a list of n_tables tensors, as the
+    reference's), which are the rows of one [n_tables, N] tensor: it remembers that tensor, so
+    the lookup can take it as it is while the list and the tensor are unchanged (the same
+    element objects, no in-place write since: the views share the tensor's version counter)."""
+
+    __slots__ = ("stacked", "views", "version")
+
+    def __init__(self, stacked):
+        views = stacked.unbind(0)
+        super().__init__(views)
+        self.views = views
+        self.stacked = stacked.reshape(len(views), -1)
+        self.version = stacked._version
+
+    def unchanged(self):
+        return (len(self) == len(self.views) and self.stacked._version == self.version
+                and all(a is b for a, b in zip(self, self.views)))
+
+
 class _GateResidual(torch.autograd.Function):
     """hidden + the gated projection of the memory vectors (module.py:239-261) with its
     gradients: the HIP backward gives the gradients of hidden, of the key / value Linear
@@ -271,7 +291,7 @@ class MicroEngram(nn.Module):
         pos = position_ids.to(input_ids.device) if position_ids is not None else None
         idx = ops.hash_ids(input_ids, pos, canon, mults, self._table_orders, self.table_rows,
                            int(self.pad_id), ident)
-        return list(idx.unbind(0))
+        return list(idx.unbind(0)) if torch.compiler.is_compiling() else _RowIds(idx)
 
     def hash_prev(self, ids):
         """Row ids from [N, W] ids of each token and its predecessors, -1 where missing: list of
@@ -279,7 +299,7 @@ class MicroEngram(nn.Module):
         canon, mults, ident = self._hash_consts(ids.device)
         idx = ops.hash_prev(ids, canon, mults, self._table_orders, self.table_rows,
                             int(self.pad_id), ident)
-        return list(idx.unbind(0))
+        return list(idx.unbind(0)) if torch.compiler.is_compiling() else _RowIds(idx)
 
     # -------------------------------------------------------------------------------- lookup
     @staticmethod
@@ -290,6 +310,8 @@ class MicroEngram(nn.Module):
         unbind of one buffer followed by its stack."""
         if torch.compiler.is_compiling():
             return torch.stack([i.reshape(-1).long() for i in idx])
+        if isinstance(idx, _RowIds) and idx.unchanged():
+            return idx.stacked
         first = idx[0]
         n = first.numel()
         storage = first.untyped_storage().data_ptr()

@@ -680,6 +680,20 @@ def dedup_keys(keys, key_bound):
     return [uniq, inv, count, plan]
 
 
+def dedup_table_bounds(uniq, count, offsets):
+    """(local rows [n] int64, info [n_tables + 2] int64) of an ascending unique-key array over
+    concatenated tables with the given host offsets (n_tables + 1, from 0): each unique key's row
+    in its own table, and info = [count, first index of each table, ..., count] -- the
+    searchsorted bounds of rows.py:123-129, in one launch."""
+    dev = require_gpu(uniq, count)
+    n = uniq.numel()
+    out = torch.empty(n + len(offsets) + 1, dtype=torch.int64, device=dev)
+    local, info = out[:n], out[n:]
+    call("me_dedup_table_bounds", _p(uniq) if n else None, n, count.data_ptr(), i64_array(list(offsets)),
+         len(offsets) - 1, _p(local) if n else None, info.data_ptr(), stream_of(dev))
+    return local, info
+
+
 def dedup_sums(plan, count, grads):
     """fp32 [n, D]: row u = the index_add_ sum of the gradient rows of unique key u (rows.py:117-118),
     from the plan and count of dedup_keys on the same n keys; rows past the count are unset."""

@@ -27,6 +27,43 @@ def stochastic_bf16(x, seed=None, step=0, stream_id=0):
     return ops.stochastic_bf16(x, seed, step, stream_id)
 
 
+class SparseBatch:
+    """The sparse gradients one row-lookup backward leaves on its tables: every table's
+    (rows, sums) is a slice of the same two buffers (unique local rows, fp32 sums), at the
+    bounds of that backward. Consumers that see a table's sparse_grad still be the exact tuple
+    handed out here (nothing replaced it since) may address all tables from the two buffers at
+    once -- the optimizer's pointer arrays and the clip's one reduction -- instead of touching
+    each table's slices."""
+
+    __slots__ = ("rows", "sums", "bounds", "handed", "__weakref__")
+
+    def __init__(self, rows, sums, bounds):
+        self.rows, self.sums, self.bounds = rows, sums, bounds
+        self.handed = {}
+
+    def member(self, shard, k, rows, sums):
+        grad = (rows, sums)
+        self.handed[k] = grad
+        shard.__dict__["_sparse_batch"] = (self, k)
+        return grad
+
+    @staticmethod
+    def common(params):
+        """The batch every param's sparse_grad still comes from, with each param's table index,
+        or (None, None)."""
+        batch, ks = None, []
+        for p in params:
+            ref = p.__dict__.get("_sparse_batch")
+            if ref is None:
+                return None, None
+            b, k = ref
+            if (batch is not None and b is not batch) or b.handed.get(k) is not getattr(p, "sparse_grad", None):
+                return None, None
+            batch = b
+            ks.append(k)
+        return batch, ks
+
+
 class LazyAdamW(torch.optim.Optimizer):
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, lazy=False,
                  rowwise=False, stochastic_rounding=True, seed=None):
@@ -36,6 +73,22 @@ class LazyAdamW(torch.optim.Optimizer):
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, lazy=lazy,
                                       rowwise=rowwise, stochastic_rounding=stochastic_rounding))
         self.seed = int(torch.randint(0, 2**62, (1,)).item()) if seed is None else int(seed)
+
+    def load_state_dict(self, state_dict):
+        """torch.optim's load, which casts every floating state tensor to its parameter's
+        dtype; the row-wise second moment (one fp32 value per row of a table) is then put back
+        from the saved fp32 values, since cast to a bf16 table's dtype it would lose what the
+        row-wise update accumulates."""
+        saved = state_dict["state"]
+        ids = [i for g in state_dict["param_groups"] for i in g["params"]]
+        super().load_state_dict(state_dict)
+        params = [p for g in self.param_groups for p in g["params"]]
+        for i, p in zip(ids, params):
+            v = saved.get(i, {}).get("exp_avg_sq")
+            if torch.is_tensor(v) and v.is_floating_point() and v.dim() == 1 and p.dim() >= 2:
+                self.state[p]["exp_avg_sq"] = v.detach().to(dtype=torch.float32, device=p.device,
+                                                             copy=True)
+        self._plans = {}
 
     @staticmethod
     def init_state(state, p, group):
@@ -102,6 +155,54 @@ class LazyAdamW(torch.optim.Optimizer):
         plan = plans[gi] = {"key": key, "members": members, "batches": list(batches.values())}
         return plan
 
+    def _advance_steps(self, gi, group, live):
+        """Adds 1 to the step counter of every live parameter and returns the new values. The
+        counters are CPU tensors, as torch.optim.AdamW keeps them; those of a group are views
+        into one buffer of the group (adopted on first sight, and again after anything put a
+        tensor of its own in their place, e.g. load_state_dict), so the usual step -- every
+        parameter live -- is one add and one host read."""
+        bufs = self.__dict__.setdefault("_step_bufs", {})
+        params = group["params"]
+        entry = bufs.get(gi)
+        if entry is None or entry[2] != tuple(id(p) for p in params):
+            buf = torch.zeros(len(params), dtype=torch.float32)
+            entry = bufs[gi] = (buf, [buf[i] for i in range(len(params))], tuple(id(p) for p in params))
+        buf, views, _ = entry
+        if len(live) == len(params) and all(a is b for a, b in zip(live, params)):
+            states = [self.state[p] for p in params]
+            for i, st in enumerate(states):
+                if st["step"] is not views[i]:
+                    step = st["step"]
+                    if step.device.type != "cpu" or step.numel() != 1:
+                        step = step.detach().reshape(()).cpu()
+                    views[i].copy_(step.float())
+                    st["step"] = views[i]
+            buf.add_(1)
+            return buf.tolist()
+        counters = [self.state[p]["step"] for p in live]
+        for c in counters:
+            c.add_(1)
+        return [float(c) for c in counters]
+
+    @staticmethod
+    def _batch_pointers(b, live, step_of):
+        """The launch's row / gradient pointer arrays straight from a SparseBatch when every
+        member's sparse gradient is still its slice of one row-lookup backward (the tables of a
+        training step): (held tensors, row ptrs, grad ptrs, counts, steps), or None."""
+        members = [live[i] for i in b["pos"]]
+        batch, ks = SparseBatch.common(members)
+        if batch is None:
+            return None
+        rows, sums = batch.rows, batch.sums
+        if (rows.dtype != torch.int64 or sums.dtype != torch.float32 or not rows.is_contiguous()
+                or not sums.is_contiguous() or sums.dim() != 2 or sums.shape[1] != b["dim"]
+                or rows.device != b["device"] or sums.device != b["device"]):
+            return None
+        bnd, dim = batch.bounds, b["dim"]
+        rb, gb = rows.data_ptr(), sums.data_ptr()
+        return ([rows, sums], [rb + bnd[k] * 8 for k in ks], [gb + bnd[k] * dim * 4 for k in ks],
+                [bnd[k + 1] - bnd[k] for k in ks], [int(step_of[i]) for i in b["pos"]])
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -116,18 +217,14 @@ class LazyAdamW(torch.optim.Optimizer):
             for p in live:
                 if not self.state[p]:
                     self.init_state(self.state[p], p, group)
-            # every step counter in one call, and one host read for all of them (the
-            # counters are CPU tensors, as torch.optim.AdamW keeps them)
-            counters = [self.state[p]["step"] for p in live]
-            torch._foreach_add_(counters, 1)
-            try:
-                step_of = torch.stack(counters).tolist()
-            except RuntimeError:  # counters loaded onto different devices
-                step_of = [float(c) for c in counters]
+            step_of = self._advance_steps(gi, group, live)
             plan = self._launch_plan(gi, group, live)
             for b in plan["batches"]:
                 dim, held, rp, gp, counts, steps = b["dim"], [], [], [], [], []
-                for j, i in enumerate(b["pos"]):
+                fast = self._batch_pointers(b, live, step_of) if group["lazy"] else None
+                if fast is not None:
+                    held, rp, gp, counts, steps = fast
+                for j, i in enumerate(b["pos"] if fast is None else ()):
                     p = live[i]
                     sparse = getattr(p, "sparse_grad", None)
                     if sparse is not None:

@@ -15,7 +15,7 @@ import threading
 import torch
 
 from . import ops
-from .optim import LazyAdamW
+from .optim import LazyAdamW, SparseBatch
 
 ROWS_DIR = "micro_engram_rows"              # complete engram (tables + the rest), DCP (rows.py:27)
 ROWS_OPTIM_DIR = "micro_engram_rows_optim"  # the tables' optimizer state, DCP (rows.py:28)
@@ -97,19 +97,6 @@ def _lookup_keys(idx2d, offs):
     return keys
 
 
-def _table_bounds(uniq_all, count, offs_all):
-    """Each unique key's row in its own table, and [count, bounds of every table in the unique
-    keys] on the device: keys past the count are masked to the largest int64, so a search over
-    the whole output stops at the count. A few launches for all tables; past the count the
-    local rows are unused."""
-    count = count.reshape(1)
-    valid = torch.arange(uniq_all.numel(), device=uniq_all.device) < count
-    masked = torch.where(valid, uniq_all, torch.iinfo(torch.int64).max)
-    offs = offs_all[:-1]
-    local_all = masked - offs[torch.searchsorted(offs, masked, right=True) - 1]
-    return local_all, torch.cat([count, torch.searchsorted(masked, offs_all)])
-
-
 class _KeyPlan:
     """The key half of a row lookup's dedup (unique keys, inverse, segment plan; torch.unique of
     rows.py:81) and the tables' bounds in it, made once: at the lookup, or when the launches
@@ -125,7 +112,7 @@ class _KeyPlan:
             offs_all = _offsets_on(self.offsets, self.idx2d.device)
             keys = _lookup_keys(self.idx2d, offs_all[:-1])
             self.outs = ops.dedup_keys(keys, int(self.offsets[-1]))
-            self.local_all, info = _table_bounds(self.outs[0], self.outs[2], offs_all)
+            self.local_all, info = ops.dedup_table_bounds(self.outs[0], self.outs[2], self.offsets)
             self.host = torch.empty(info.shape, dtype=info.dtype, pin_memory=True)
             self.host.copy_(info, non_blocking=True)
             self.ready = torch.cuda.Event()
@@ -203,13 +190,14 @@ class _RowLookup(torch.autograd.Function):
         else:
             outs = ops.dedup(_lookup_keys(idx2d, offs), int(ctx.offsets[-1]), grad.reshape(n * nt, D))
             # one host read for the unique count and every table's bounds
-            local_all, info = _table_bounds(outs[0], outs[2], offs_all)
+            local_all, info = ops.dedup_table_bounds(outs[0], outs[2], ctx.offsets)
             host = info.tolist()
         cnt, bounds = host[0], host[1:]
         # each table's slice of the unique rows and sums (bounds[0] = 0, bounds[nt] = count)
         sizes = [bounds[k + 1] - bounds[k] for k in range(nt)]
         locals_ = local_all[:cnt].split(sizes)
         sums = outs[3][:cnt].split(sizes)
+        batch = SparseBatch(local_all[:cnt], outs[3][:cnt], bounds)
         grads = []
         for k, (shape, dtype) in enumerate(ctx.shapes):
             if not ctx.needs_input_grad[2 + k]:
@@ -221,7 +209,7 @@ class _RowLookup(torch.autograd.Function):
                     # this table's part of the dedup is already coalesced: unique rows in
                     # ascending order and fp32 sums that start from +0.0, as index_add_'s do
                     # (what add_sparse_grad would return for it, without a second dedup)
-                    shard.sparse_grad = (locals_[k], sums[k])
+                    shard.sparse_grad = batch.member(shard, k, locals_[k], sums[k])
                 else:
                     add_sparse_grad(shard, locals_[k], sums[k])
                 grads.append(None)
@@ -278,6 +266,16 @@ class RowTables:
         if not ps:
             return None
         sq = torch.zeros(1, dtype=torch.float32, device=ps[0].device)
+        batch, ks = SparseBatch.common(ps) if all(p.grad is None for p in ps) else (None, None)
+        if (batch is not None and sorted(ks) == list(range(len(batch.bounds) - 1))
+                and batch.sums.is_contiguous() and batch.sums.data_ptr() % 16 == 0):
+            # every table's gradient is its slice of one backward's sums, which tile them
+            span = batch.sums.reshape(-1)
+            ops.sumsq(span, sq, accumulate=True)
+            if max_norm and max_norm > 0:
+                ops.clip_scale(span, sq, max_norm)
+            self.last_grad_norm = float(sq.sqrt().item())
+            return self.last_grad_norm
         squares, scaled = [], []
         for p in ps:
             if p.grad is not None:
@@ -314,6 +312,7 @@ class RowTables:
             self.optimizer.zero_grad(set_to_none=True)
         for p in self.params():
             p.sparse_grad = None
+            p.__dict__.pop("_sparse_batch", None)
 
     # --- checkpoints: DCP folders (rows.py:257-343 fixes their names and contents) ---------
     def _trainable_tables(self, include_frozen=False):

@@ -598,3 +598,67 @@ def test_bf16_second_moment_freeze_vs_stochastic_rounding():
             opt.step()
         out[name] = float(opt.state[p]["exp_avg_sq"].float().mean()) / (1 - 0.999 ** 1500)
     assert out["plain"] < 0.5 and abs(out["sr"] - 1) < 0.02 and abs(out["rowwise"] - 1) < 1e-4
+
+
+@pytest.mark.parametrize("case", ["random", "empty_tables", "zero_count", "boundaries"])
+def test_dedup_table_bounds(case):
+    # the one-launch bounds against numpy's searchsorted over the unique keys (rows.py:123-129):
+    # every unique key's local row and each table's first index, with empty tables, a count
+    # below the array length and keys right at the table boundaries
+    g = torch.Generator().manual_seed(len(case))
+    sizes = [97, 0, 5, 1 << 20, 3, 0, 1000] if case == "empty_tables" else [131, 257, 97, 4099]
+    offs = [0]
+    for r in sizes:
+        offs.append(offs[-1] + r)
+    if case == "boundaries":
+        keys = torch.tensor(sorted(set(offs[:-1]) | {o - 1 for o in offs[1:]}), dtype=torch.int64)
+    else:
+        keys = torch.unique(torch.randint(0, offs[-1], (600,), generator=g))
+    n = keys.numel() + 7  # slots past the count, as the dedup output has
+    uniq = torch.full((n,), -5, dtype=torch.int64)
+    uniq[:keys.numel()] = keys
+    cnt = 0 if case == "zero_count" else keys.numel()
+    local, info = ops.dedup_table_bounds(uniq.to(DEV), torch.tensor([cnt], device=DEV), offs)
+    valid = uniq[:cnt].numpy()
+    want_bounds = np.searchsorted(valid, np.array(offs), side="left")
+    assert info.cpu().tolist() == [cnt] + want_bounds.tolist()
+    tbl = np.searchsorted(np.array(offs[:-1]), valid, side="right") - 1
+    assert np.array_equal(local.cpu().numpy()[:cnt], valid - np.array(offs)[tbl])
+
+
+def test_training_step_fast_paths_equal_the_general_ones():
+    # the clip and the optimizer address a backward's per-table sparse gradients through the
+    # buffers they are slices of (SparseBatch); with that link removed they take the general
+    # per-table paths. Two identical engrams, three training steps each (norms, tables, both
+    # moments, step counters): bit for bit. The third step of the general run also reloads the
+    # optimizer state, so the shared step-counter buffer is re-adopted from loaded tensors.
+    def run(general):
+        torch.manual_seed(3)  # the dense tables' init draws from the global generator
+        eng = MicroEngram(model_dim=64, table_size=211, engram_dim=8, num_heads=2, orders=(2, 3, 4),
+                          vocab_size=1000, gate="scalar_sqrt", seed=3)
+        synthetic.fill_dense(eng, seed=3, std=0.2)
+        eng = eng.to(DEV)
+        eng.shard_rows(0, 1, device=DEV, dtype=torch.bfloat16)
+        rt = me_rows.RowTables([("e.", eng)], lr=5e-3, lazy=True, rowwise=True, sparse_grads=True, seed=11)
+        gen = torch.Generator().manual_seed(4)
+        norms = []
+        for k in range(3):
+            ids = torch.randint(0, 40, (2, 60), generator=gen).to(DEV)
+            h = torch.randn(2, 60, 64, generator=gen).to(DEV).requires_grad_(True)
+            eng(h, ids).backward(torch.randn(2, 60, 64, generator=gen).to(DEV))
+            if general:
+                for p in eng.row_shards:
+                    p.__dict__.pop("_sparse_batch", None)
+                if k == 2:
+                    rt.optimizer.load_state_dict(rt.optimizer.state_dict())
+            norms.append(rt.clip(0.05))
+            rt.step(5e-3)
+        st = rt.optimizer.state
+        return norms, [(p.detach().clone(), st[p]["exp_avg"].clone(), st[p]["exp_avg_sq"].clone(),
+                        float(st[p]["step"])) for p in eng.row_shards]
+
+    fast_norms, fast = run(False)
+    gen_norms, general = run(True)
+    assert fast_norms == gen_norms
+    for (p1, m1, v1, s1), (p2, m2, v2, s2) in zip(fast, general):
+        assert torch.equal(p1, p2) and torch.equal(m1, m2) and torch.equal(v1, v2) and s1 == s2 == 3.0

@@ -38,3 +38,25 @@ def test_spans_never_extend_a_strided_span():
     # a contiguous 1-D span followed by its neighbour still merges
     merged = _spans([buf[:6], buf[6:9]])
     assert len(merged) == 1 and torch.equal(merged[0], buf[:9])
+
+
+def test_optimizer_load_keeps_the_row_wise_second_moment_fp32():
+    # torch.optim's load casts floating state to the parameter's dtype; the row-wise second
+    # moment of a bf16 table keeps its fp32 values (1 + 1e-4 is not a bf16 number)
+    from micro_engram_fork_amd.optim import LazyAdamW
+    table = torch.nn.Parameter(torch.zeros(5, 4, dtype=torch.bfloat16))
+    bias = torch.nn.Parameter(torch.zeros(3, dtype=torch.bfloat16))
+    opt = LazyAdamW([table, bias], lazy=True, rowwise=True, seed=1)
+    for p in (table, bias):
+        st = opt.state[p]
+        LazyAdamW.init_state(st, p, opt.param_groups[0])
+        st["step"] = torch.tensor(3.0)
+        st["exp_avg_sq"] += 1.0001
+    loaded = LazyAdamW([table, bias], lazy=True, rowwise=True, seed=1)
+    loaded.load_state_dict(opt.state_dict())
+    row = loaded.state[table]
+    assert row["exp_avg_sq"].dtype == torch.float32 and row["exp_avg_sq"].shape == (5,)
+    assert torch.equal(row["exp_avg_sq"], opt.state[table]["exp_avg_sq"])
+    assert row["exp_avg_sq"] is not opt.state[table]["exp_avg_sq"]
+    assert row["exp_avg"].dtype == torch.bfloat16 and float(row["step"]) == 3.0
+    assert loaded.state[bias]["exp_avg_sq"].dtype == torch.bfloat16  # elementwise: torch's cast
