@@ -296,6 +296,25 @@ int me_gate_backward(const void *hidden, int hidden_dtype, int64_t n, int64_t mo
 int me_dedup_workspace_size(int64_t n, size_t *bytes);
 
 /*
+ * me_linear_grads -- gradients of the engram's key / value Linear layers from the gradients of
+ * their outputs (what autograd computes for the two nn.Linear calls of the reference's forward,
+ * micro_engram/module.py:245, 254; here after me_gate_backward):
+ *
+ *   grad_mem     [n, mem_dim]   = grad_key . w_key + grad_value . w_value
+ *   grad_w_key   [model_dim, mem_dim] = grad_key^T . mem;  grad_w_value = grad_value^T . mem
+ *
+ *   grad_key, grad_value   [n, model_dim] bf16 (me_gate_backward's outputs)
+ *   mem           [n, mem_dim] bf16, w_key / w_value [model_dim, mem_dim] bf16
+ *   outputs bf16, any of them NULL to skip it; fp32 accumulation over the whole reduction (both
+ *   products of grad_mem in one sum), one round to nearest even per element. n == 0 leaves
+ *   zero weight gradients. model_dim and mem_dim multiples of 8 (of 64 for grad_mem), every
+ *   operand under 2 GiB and 16-byte aligned.
+ */
+int me_linear_grads(const void *grad_key, const void *grad_value, int64_t n, int64_t model_dim,
+                    const void *mem, int64_t mem_dim, const void *w_key, const void *w_value,
+                    void *grad_mem, void *grad_w_key, void *grad_w_value, void *stream);
+
+/*
  * me_dedup -- touched-row dedup with coalesced gradients.
  * Replaces torch.unique(flat, return_inverse=True) and zeros(n_uniq, D).index_add_(0, inv, g)
  * (micro_engram/rows.py:81, 117-118; add_sparse_grad rows.py:137-147).

@@ -44,6 +44,8 @@ SIGNATURES = {
     "me_gate_backward": [c_ptr, c_int, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_int,
                          c_ptr, c_ptr, c_int, c_int, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
                          c_ptr, c_ptr, c_ptr, c_size, c_ptr],
+    "me_linear_grads": [c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+                        c_ptr],
     "me_dedup_workspace_size": [c_i64, ctypes.POINTER(c_size)],
     "me_dedup": [c_ptr, c_i64, c_i64, c_ptr, c_int, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
                  c_size, c_ptr],

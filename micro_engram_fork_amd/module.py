@@ -75,8 +75,8 @@ class _RowIds(list):
 class _GateResidual(torch.autograd.Function):
     """hidden + the gated projection of the memory vectors (module.py:239-261) with its
     gradients: the HIP backward gives the gradients of hidden, of the key / value Linear
-    outputs and of the scale deltas; the Linear layers' own gradients are plain GEMMs
-    (dW = dY^T mem, dmem = dY_K W_K + dY_V W_V) on the library BLAS."""
+    outputs and of the scale deltas; the Linear layers' own gradients (dW = dY^T mem,
+    dmem = dY_K W_K + dY_V W_V) come from _linear_grads."""
 
     @staticmethod
     def forward(ctx, hidden, mem, w_key, w_value, q_delta, k_delta, gate_mode, keep):
@@ -98,13 +98,29 @@ class _GateResidual(torch.autograd.Function):
             grad_out.contiguous(), hidden.detach(), mem.detach(), wk, wv,
             None if q_delta is None else q_delta.detach(),
             None if k_delta is None else k_delta.detach(), ctx.gate_mode, keep, stats)
-        m = mem.detach().reshape(g_key.shape[0], -1)
-        d_mem = torch.addmm(g_key @ wk, g_value, wv).reshape(mem.shape) if need[1] else None
-        d_wk = g_key.t() @ m if need[2] else None
-        d_wv = g_value.t() @ m if need[3] else None
+        d_mem, d_wk, d_wv = _linear_grads(g_key, g_value, mem.detach(), wk, wv, need[1:4])
         d_q = g_q.to(q_delta.dtype) if need[4] else None
         d_k = g_k.to(k_delta.dtype) if need[5] else None
         return g_hidden if need[0] else None, d_mem, d_wk, d_wv, d_q, d_k, None, None
+
+
+def _linear_grads(g_key, g_value, mem, wk, wv, need):
+    """Gradients of the key / value Linear layers from those of their outputs (autograd's
+    nn.Linear backward for module.py:245, 254): d_mem = dK W_K + dV W_V and dW = dY^T mem, each
+    None where `need` (mem, w_key, w_value) says so. bf16 shapes the hand-written MFMA kernel
+    takes run on it (me_linear_grads); others on the library GEMMs."""
+    if not any(need):
+        return None, None, None
+    n, M = g_key.shape[0], mem.shape[-1]
+    m = mem.reshape(n, M)
+    if ops.fits_linear_grads(n, g_key.shape[1], M, m.dtype) and wk.dtype == wv.dtype == g_key.dtype == m.dtype:
+        d_mem, d_wk, d_wv = ops.linear_grads(g_key, g_value, m, wk, wv, *need)
+        return (d_mem.reshape(mem.shape) if need[0] else None, d_wk if need[1] else None,
+                d_wv if need[2] else None)
+    d_mem = torch.addmm(g_key @ wk, g_value, wv).reshape(mem.shape) if need[0] else None
+    d_wk = g_key.t() @ m if need[1] else None
+    d_wv = g_value.t() @ m if need[2] else None
+    return d_mem, d_wk, d_wv
 
 
 class _GateResidualRows(torch.autograd.Function):
@@ -135,10 +151,7 @@ class _GateResidualRows(torch.autograd.Function):
             grad_out.contiguous(), hidden.detach(), k, v,
             None if q_delta is None else q_delta.detach(),
             None if k_delta is None else k_delta.detach(), ctx.gate_mode, keep, stats)
-        m = mem.detach().reshape(g_key.shape[0], -1)
-        d_mem = torch.addmm(g_key @ wk, g_value, wv).reshape(mem.shape) if need[1] else None
-        d_wk = g_key.t() @ m if need[2] else None
-        d_wv = g_value.t() @ m if need[3] else None
+        d_mem, d_wk, d_wv = _linear_grads(g_key, g_value, mem.detach(), wk, wv, need[1:4])
         d_q = g_q.to(q_delta.dtype) if need[4] else None
         d_k = g_k.to(k_delta.dtype) if need[5] else None
         return g_hidden if need[0] else None, d_mem, d_wk, d_wv, d_q, d_k, None, None

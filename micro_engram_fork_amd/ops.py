@@ -607,6 +607,58 @@ def _(grad_out, hidden, mem, w_key, w_value, q_scale_delta, k_scale_delta, gate_
             hidden.new_empty((nd,), dtype=torch.float32), hidden.new_empty((nd,), dtype=torch.float32)]
 
 
+def fits_linear_grads(n, model_dim, mem_dim, dtype):
+    """Whether me_linear_grads takes the key / value Linear layers' gradients: bf16 operands,
+    model dim a multiple of 64, memory width a multiple of 8, every operand under 2 GiB. Other
+    shapes and fp32 engrams take the library GEMMs."""
+    lim = 1 << 31
+    return (dtype == torch.bfloat16 and model_dim % 64 == 0 and mem_dim % 8 == 0 and
+            n * model_dim * 2 < lim and n * mem_dim * 2 < lim and model_dim * mem_dim * 2 < lim)
+
+
+@_custom_op("linear_grads")
+def linear_grads(grad_key: torch.Tensor, grad_value: torch.Tensor, mem: torch.Tensor,
+                 w_key: torch.Tensor, w_value: torch.Tensor, need_mem: bool, need_w_key: bool,
+                 need_w_value: bool) -> List[torch.Tensor]:
+    """[grad_mem [N, M], grad_w_key [d, M], grad_w_value [d, M]] (an empty tensor for each one
+    not needed): the gradients autograd gives the two nn.Linear calls of the reference's
+    forward (micro_engram/module.py:245, 254) from the gradients of their outputs,
+    grad_mem = gK W_K + gV W_V and grad_W = g^T mem, on the hand-written MFMA kernel. bf16."""
+    dev = require_gpu(grad_key, grad_value, mem, w_key, w_value)
+    n, d = grad_key.shape
+    M = mem.shape[-1]
+    if grad_value.shape != (n, d) or mem.numel() != n * M or w_key.shape != (d, M) or w_value.shape != (d, M):
+        raise ValueError(f"[micro_engram] linear_grads: shapes {tuple(grad_key.shape)}, "
+                         f"{tuple(grad_value.shape)}, {tuple(mem.shape)}, {tuple(w_key.shape)}, "
+                         f"{tuple(w_value.shape)} do not match")
+    if any(t.dtype != torch.bfloat16 for t in (grad_key, grad_value, mem, w_key, w_value)):
+        raise ValueError("[micro_engram] linear_grads takes bf16 operands")
+
+    def ready(t):
+        t = t.contiguous()
+        return t if _aligned(t) else t.clone()
+
+    gk, gv, m, wk, wv = (ready(t) for t in (grad_key, grad_value, mem.reshape(n, M), w_key, w_value))
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    d_mem = torch.empty((n, M) if need_mem else (0,), **bf)
+    d_wk = torch.empty((d, M) if need_w_key else (0,), **bf)
+    d_wv = torch.empty((d, M) if need_w_value else (0,), **bf)
+    call("me_linear_grads", gk.data_ptr(), gv.data_ptr(), n, d, m.data_ptr(), M, wk.data_ptr(),
+         wv.data_ptr(), d_mem.data_ptr() if need_mem else None,
+         d_wk.data_ptr() if need_w_key else None, d_wv.data_ptr() if need_w_value else None,
+         stream_of(dev))
+    return [d_mem, d_wk, d_wv]
+
+
+@linear_grads.register_fake
+def _(grad_key, grad_value, mem, w_key, w_value, need_mem, need_w_key, need_w_value):
+    n, d = grad_key.shape
+    M = mem.shape[-1]
+    return [grad_key.new_empty((n, M) if need_mem else (0,)),
+            grad_key.new_empty((d, M) if need_w_key else (0,)),
+            grad_key.new_empty((d, M) if need_w_value else (0,))]
+
+
 def library_loaded():
     """Loads the HIP library (raises if it is missing) and returns its path."""
     _lib.load()
