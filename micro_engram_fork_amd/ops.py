@@ -67,8 +67,19 @@ def _direct_call(args, kwargs):
     """Whether a call may skip the op's dispatch: nothing is tracing (dynamo), no dispatch mode
     is active (make_fx, FlopCounterMode, debug or recording modes see only the dispatcher) and
     every tensor argument is a plain tensor (fake tensors and other subclasses need the op)."""
-    return (not torch.compiler.is_compiling() and torch._C._len_torch_dispatch_stack() == 0
-            and all(_plain(a) for a in args) and all(_plain(v) for v in kwargs.values()))
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack():  # this order: dynamo
+        return False                                                           # folds the first
+    for a in (*args, *kwargs.values()) if kwargs else args:
+        tp = type(a)
+        if tp in _PLAIN_TENSORS or a is None:
+            continue
+        if tp is list or tp is tuple:
+            for v in a:
+                if isinstance(v, torch.Tensor) and type(v) not in _PLAIN_TENSORS:
+                    return False
+        elif isinstance(a, torch.Tensor):
+            return False
+    return True
 
 
 def _custom_op(name):
@@ -128,6 +139,12 @@ def _canon_ptr(canon, identity):
 
 
 def _table_args(table_orders, table_rows):
+    return _table_args_of(tuple(table_orders), tuple(table_rows))
+
+
+@functools.lru_cache(maxsize=64)
+def _table_args_of(table_orders, table_rows):
+    # ctypes arrays the kernels only read: one per distinct table layout
     return len(table_orders), i32_array(list(table_orders)), i64_array(list(table_rows))
 
 
@@ -187,7 +204,22 @@ def _(ids, canon, mults, table_orders, table_rows, pad_id, identity_canon=False)
 
 
 # ------------------------------------------------------------------------------------- gather
+_TABLES_ARGS = {}
+
+
 def _tables_arg(tables: Sequence[torch.Tensor]):
+    """(pointer array, row counts, row width) of the tables, checked: kept per (address, shape,
+    strides, dtype) of every table, which fix all three (the arrays are only read)."""
+    key = tuple((t.data_ptr(), t.shape, t.stride(), t.dtype) for t in tables)
+    hit = _TABLES_ARGS.get(key)
+    if hit is None:
+        if len(_TABLES_ARGS) >= 256:
+            _TABLES_ARGS.clear()
+        hit = _TABLES_ARGS[key] = _tables_arg_checked(tables)
+    return hit
+
+
+def _tables_arg_checked(tables):
     t0 = tables[0]
     dim = t0.shape[1]
     for t in tables:

@@ -203,8 +203,48 @@ class LazyAdamW(torch.optim.Optimizer):
         return ([rows, sums], [rb + bnd[k] * 8 for k in ks], [gb + bnd[k] * dim * 4 for k in ks],
                 [bnd[k + 1] - bnd[k] for k in ks], [int(step_of[i]) for i in b["pos"]])
 
+    def step(self, *args, **kwargs):
+        """One step (closure: optional, as torch.optim's). torch.optim wraps an optimizer's step
+        in a profiler range and its step hooks; that range is a dispatched op (~25 us of host
+        time per step, paid with no profiler running, on a training step bound by its host's
+        issue rate), so this optimizer runs the hooks itself, with the same order and return
+        rules, and opens the range only while the autograd profiler is on."""
+        if torch.autograd.profiler._is_profiler_enabled:
+            with torch.autograd.profiler.record_function(f"Optimizer.step#{type(self).__name__}.step"):
+                return self._hooked_step(args, kwargs)
+        return self._hooked_step(args, kwargs)
+
+    step.hooked = True  # torch.optim.Optimizer leaves a step marked so unwrapped
+
+    def _hooked_step(self, args, kwargs):
+        from torch.optim.optimizer import _global_optimizer_post_hooks, _global_optimizer_pre_hooks
+
+        for pre_hook in (*_global_optimizer_pre_hooks.values(), *self._optimizer_step_pre_hooks.values()):
+            result = pre_hook(self, args, kwargs)
+            if result is not None:
+                if isinstance(result, tuple) and len(result) == 2:
+                    args, kwargs = result
+                else:
+                    raise RuntimeError(f"optimizer step pre-hooks must return None or a tuple of "
+                                       f"(new_args, new_kwargs), but got {result}.")
+        out = self._step(*args, **kwargs)
+        self._optimizer_step_code()
+        for post_hook in (*self._optimizer_step_post_hooks.values(), *_global_optimizer_post_hooks.values()):
+            post_hook(self, args, kwargs)
+        return out
+
+    def zero_grad(self, set_to_none=True):
+        """torch.optim's zero_grad; with set_to_none (the default) without its profiler range
+        (opened only while the autograd profiler is on, as for step)."""
+        if not set_to_none or torch.autograd.profiler._is_profiler_enabled:
+            return super().zero_grad(set_to_none)
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is not None:
+                    p.grad = None
+
     @torch.no_grad()
-    def step(self, closure=None):
+    def _step(self, closure=None):
         loss = None
         if closure is not None:
             with torch.enable_grad():

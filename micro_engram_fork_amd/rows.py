@@ -113,7 +113,7 @@ class _KeyPlan:
             keys = _lookup_keys(self.idx2d, offs_all[:-1])
             self.outs = ops.dedup_keys(keys, int(self.offsets[-1]))
             self.local_all, info = ops.dedup_table_bounds(self.outs[0], self.outs[2], self.offsets)
-            self.host = torch.empty(info.shape, dtype=info.dtype, pin_memory=True)
+            self.host = _pinned_take(info.numel())
             self.host.copy_(info, non_blocking=True)
             self.ready = torch.cuda.Event()
             self.ready.record(torch.cuda.current_stream(info.device))  # the copy's stream
@@ -124,7 +124,26 @@ class _KeyPlan:
         """(local rows of the unique keys, [count, table bounds] as host ints)."""
         self.make()
         self.ready.synchronize()
-        return self.local_all, self.host.tolist()
+        buf, self.host = self.host, None
+        host = buf.tolist()
+        _pinned_give(buf)  # its copy is done and read (a plan that is never read keeps its own)
+        return self.local_all, host
+
+
+_PINNED = {}
+
+
+def _pinned_take(n):
+    """A pinned int64 host buffer of n values from the pool (allocating pinned memory is a
+    host-allocator call on every step otherwise)."""
+    free = _PINNED.get(n)
+    return free.pop() if free else torch.empty(n, dtype=torch.int64, pin_memory=True)
+
+
+def _pinned_give(t):
+    free = _PINNED.setdefault(t.numel(), [])
+    if len(free) < 8:
+        free.append(t)
 
 
 _PLANS = threading.local()
@@ -160,7 +179,7 @@ class _RowLookup(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, idx2d, offsets, *shards):
-        mem = ops.gather(idx2d, [s.detach() for s in shards])
+        mem = ops.gather(idx2d, list(shards))  # no graph is recorded inside forward
         ctx.save_for_backward(idx2d)
         ctx.offsets = offsets
         ctx.shapes = [(s.shape, s.dtype) for s in shards]
