@@ -410,15 +410,15 @@ int me_clip_scale(void *x, int dtype, int64_t n, const float *sumsq, double max_
  *
  *   HOST arrays [n_tables]: params, exp_avgs (device [rows_k, dim], param_dtype), exp_avg_sqs
  *   (device [rows_k] fp32 or [rows_k, dim] sq_dtype), rows (device int64 [n_rows_k], unique),
- *   grads (device fp32 [n_rows_k, dim]), n_rows, steps (the step count after this step's
+ *   grads (device [n_rows_k, dim] of grad_dtype, ME_F32 or ME_BF16), n_rows, steps (the step count after this step's
  *   increment), stream_ids (< 65536, distinct per table: selects the table's rounding noise)
  * The rounding noise of element (row, col) is 16 bits of Philox4x32-10 keyed by seed with counter
  * (row low, row high, step, stream_id << 16 | which << 14 | col >> 3), word (col >> 1) & 3,
  * half col & 1; which = 0 weights, 1 first moment, 2 per-value second moment.
  */
 int me_sparse_adam(int32_t n_tables, void *const *params, void *const *exp_avgs,
-                   void *const *exp_avg_sqs, const int64_t *const *rows, const float *const *grads,
-                   const int64_t *n_rows, const int64_t *steps, const int32_t *stream_ids,
+                   void *const *exp_avg_sqs, const int64_t *const *rows, const void *const *grads,
+                   int grad_dtype, const int64_t *n_rows, const int64_t *steps, const int32_t *stream_ids,
                    int32_t dim, int param_dtype, int rowwise, int sq_dtype, int lazy, double lr,
                    double beta1, double beta2, double eps, double weight_decay,
                    int stochastic_rounding, uint64_t seed, void *stream);

@@ -54,7 +54,7 @@ SIGNATURES = {
     "me_dedup_table_bounds": [c_ptr, c_i64, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr],
     "me_dedup_sums": [c_ptr, c_size, c_i64, c_ptr, c_ptr, c_int, c_i32, c_ptr, c_ptr],
     "me_sumsq": [c_ptr, c_i64, c_ptr, c_int, c_ptr, c_size, c_ptr],
-    "me_sparse_adam": [c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_int,
+    "me_sparse_adam": [c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_ptr, c_ptr, c_ptr, c_i32, c_int,
                        c_int, c_int, c_int, c_double, c_double, c_double, c_double, c_double,
                        c_int, ctypes.c_uint64, c_ptr],
     "me_clip_scale": [c_ptr, c_int, c_i64, c_ptr, c_double, c_ptr],

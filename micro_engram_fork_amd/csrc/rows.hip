@@ -846,7 +846,7 @@ struct AdamTable {
     uint8_t *exp_avg;      // like param
     uint8_t *exp_avg_sq;   // row-wise: [rows] fp32; per value: like param
     const int64_t *rows;   // [n] unique row ids
-    const float *grads;    // [n, dim] fp32
+    const uint8_t *grads;  // [n, dim] fp32 or bf16 (grad_bf16)
     int64_t n;
     int64_t first;         // first global row slot of this table in the launch
     float neg_lr_bc1;      // -lr / (1 - beta1^step)
@@ -865,6 +865,7 @@ struct AdamArgs {
     int param_bf16;
     int rowwise;
     int sq_bf16;           // per-value second moment stored as bf16
+    int grad_bf16;         // gradient rows stored as bf16
     int sr;
     int lazy;              // skip rows whose gradient is all zero
     uint64_t seed;
@@ -897,12 +898,12 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
     const int64_t i = slot - t.first;
     const int64_t row = *as_global(t.rows + i);
     const int D = a.dim;
-    const float *g_row = t.grads + i * D;
+    const int64_t g_row = i * D;
     // lazy: a row whose gradient is all zero is skipped entirely (optim.py:92-95)
     bool any = false;
     float gsq = 0.f;
     for (int c = lane; c < D; c += 64) {
-        const float g = g_row[c];
+        const float g = load_elem(t.grads, a.grad_bf16, g_row + c);
         any |= g != 0.f;
         gsq += g * g;
     }
@@ -920,7 +921,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows(const AdamArgs a) {
         denom_row = sqrtf(v_row) / t.sqrt_bc2 + a.eps;
     }
     for (int c = lane; c < D; c += 64) {
-        const float g = g_row[c];
+        const float g = load_elem(t.grads, a.grad_bf16, g_row + c);
         float p = load_elem(t.param, a.param_bf16, prow + c);
         float m = load_elem(t.exp_avg, a.param_bf16, prow + c);
         if (a.has_decay) p = p * a.decay;
@@ -1033,8 +1034,9 @@ __device__ __forceinline__ void store_cols(uint8_t *base, int64_t e0, const floa
 // row's weights and moments are loaded together with its gradient, before the lazy test, so
 // that one memory round trip follows the row id's. The weight dtype (PB: bf16, else fp32) and
 // the second-moment form (RW: one fp32 per row) are template parameters: a run-time branch
-// around each load makes the compiler wait for every load before issuing the next.
-template <int LPR, int C, bool PB, bool RW>
+// around each load makes the compiler wait for every load before issuing the next. So is the
+// gradients' dtype (GB: bf16, else fp32).
+template <int LPR, int C, bool PB, bool RW, bool GB>
 __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     constexpr int kRowsPerWave = 64 / LPR;
     constexpr int kRowsPerBlock = kRowsPerWave * (kThreads / 64);
@@ -1063,7 +1065,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
     const int c0 = C * sub;
     const int64_t i = slot - t.first;
     float g[C], p[C], m[C], v[C];
-    load_cols<C, false>(reinterpret_cast<const uint8_t *>(t.grads), i * D + c0, g);
+    load_cols<C, GB>(t.grads, i * D + c0, g);
     const int64_t row = *as_global(t.rows + i);
     const int64_t e0 = row * D + c0;
     load_cols<C, PB>(t.param, e0, p);
@@ -1129,7 +1131,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows_vec(const AdamArgs a) {
 // per row walking nb blocks of 64 x C columns, the same arithmetic and noise as adam_rows_vec per
 // block. The lazy skip and the row-wise second moment need the whole row's gradient first: a
 // pass over its blocks before the update pass (which loads them again).
-template <int C, bool PB, bool RW>
+template <int C, bool PB, bool RW, bool GB>
 __global__ __launch_bounds__(kThreads) void adam_rows_wide(const AdamArgs a) {
     __shared__ AdamTable s_t[kAdamTables];
     const int tid = threadIdx.x;
@@ -1152,14 +1154,14 @@ __global__ __launch_bounds__(kThreads) void adam_rows_wide(const AdamArgs a) {
     const int D = a.dim, nb = D / (64 * C);
     const int64_t i = slot - t.first;
     const int64_t row = *as_global(t.rows + i);
-    const uint8_t *grow = reinterpret_cast<const uint8_t *>(t.grads);
+    const uint8_t *grow = t.grads;
     float v_row = 0.f, denom_row = 0.f;
     if (RW || a.lazy) {
         bool any = false;
         float gsq = 0.f;
         for (int b = 0; b < nb; ++b) {
             float g[C];
-            load_cols<C, false>(grow, i * D + b * 64 * C + lane * C, g);
+            load_cols<C, GB>(grow, i * D + b * 64 * C + lane * C, g);
 #pragma unroll
             for (int e = 0; e < C; ++e) {
                 any |= g[e] != 0.f;
@@ -1180,7 +1182,7 @@ __global__ __launch_bounds__(kThreads) void adam_rows_wide(const AdamArgs a) {
         const int c0 = b * 64 * C + lane * C;
         const int64_t e0 = row * D + c0;
         float g[C], p[C], m[C], v[C];
-        load_cols<C, false>(grow, i * D + c0, g);
+        load_cols<C, GB>(grow, i * D + c0, g);
         load_cols<C, PB>(t.param, e0, p);
         load_cols<C, PB>(t.exp_avg, e0, m);
         if constexpr (!RW) {
@@ -1585,30 +1587,47 @@ extern "C" int me_clip_scale(void *x, int dtype, int64_t n, const float *sumsq, 
     return check_launch("me_clip_scale");
 }
 
-template <int C, bool PB, bool RW>
+template <int C, bool PB, bool RW, bool GB>
 void launch_adam_vec_k(int lpr, dim3 grid, hipStream_t s, const AdamArgs &a) {
     switch (lpr) {
-        case 1: hipLaunchKernelGGL((adam_rows_vec<1, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((adam_rows_vec<2, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((adam_rows_vec<4, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((adam_rows_vec<8, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
-        case 16: hipLaunchKernelGGL((adam_rows_vec<16, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((adam_rows_vec<32, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
-        default: hipLaunchKernelGGL((adam_rows_vec<64, C, PB, RW>), grid, dim3(kThreads), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((adam_rows_vec<1, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((adam_rows_vec<2, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((adam_rows_vec<4, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((adam_rows_vec<8, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((adam_rows_vec<16, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((adam_rows_vec<32, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
+        default: hipLaunchKernelGGL((adam_rows_vec<64, C, PB, RW, GB>), grid, dim3(kThreads), 0, s, a); break;
     }
 }
 
-template <int C>
-void launch_adam_vec(int lpr, bool pb, bool rw, dim3 grid, hipStream_t s, const AdamArgs &a) {
+template <int C, bool GB>
+void launch_adam_vec_g(int lpr, bool pb, bool rw, dim3 grid, hipStream_t s, const AdamArgs &a) {
     if (pb)
-        rw ? launch_adam_vec_k<C, true, true>(lpr, grid, s, a) : launch_adam_vec_k<C, true, false>(lpr, grid, s, a);
+        rw ? launch_adam_vec_k<C, true, true, GB>(lpr, grid, s, a) : launch_adam_vec_k<C, true, false, GB>(lpr, grid, s, a);
     else
-        rw ? launch_adam_vec_k<C, false, true>(lpr, grid, s, a) : launch_adam_vec_k<C, false, false>(lpr, grid, s, a);
+        rw ? launch_adam_vec_k<C, false, true, GB>(lpr, grid, s, a) : launch_adam_vec_k<C, false, false, GB>(lpr, grid, s, a);
+}
+
+template <int C>
+void launch_adam_vec(int lpr, bool pb, bool rw, bool gb, dim3 grid, hipStream_t s, const AdamArgs &a) {
+    gb ? launch_adam_vec_g<C, true>(lpr, pb, rw, grid, s, a) : launch_adam_vec_g<C, false>(lpr, pb, rw, grid, s, a);
+}
+
+template <bool GB>
+void launch_adam_wide(bool pb, bool rw, dim3 grid, hipStream_t s, const AdamArgs &a) {
+    if (pb && rw)
+        hipLaunchKernelGGL((adam_rows_wide<8, true, true, GB>), grid, dim3(kThreads), 0, s, a);
+    else if (pb)
+        hipLaunchKernelGGL((adam_rows_wide<8, true, false, GB>), grid, dim3(kThreads), 0, s, a);
+    else if (rw)
+        hipLaunchKernelGGL((adam_rows_wide<8, false, true, GB>), grid, dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((adam_rows_wide<8, false, false, GB>), grid, dim3(kThreads), 0, s, a);
 }
 
 extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const *exp_avgs,
                               void *const *exp_avg_sqs, const int64_t *const *rows,
-                              const float *const *grads, const int64_t *n_rows,
+                              const void *const *grads, int grad_dtype, const int64_t *n_rows,
                               const int64_t *steps, const int32_t *stream_ids, int32_t dim,
                               int param_dtype, int rowwise, int sq_dtype, int lazy, double lr,
                               double beta1, double beta2, double eps, double weight_decay,
@@ -1617,6 +1636,7 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
     ME_CHECK_ARG(params && exp_avgs && exp_avg_sqs && rows && grads && n_rows && steps && stream_ids,
                  "null argument array");
     ME_CHECK_ARG(param_dtype == ME_BF16 || param_dtype == ME_F32, "param dtype must be bf16/fp32");
+    ME_CHECK_ARG(grad_dtype == ME_BF16 || grad_dtype == ME_F32, "grad dtype must be bf16/fp32");
     ME_CHECK_ARG(dim >= 1, "dim must be positive");
     ME_CHECK_ARG(rowwise || sq_dtype == ME_BF16 || sq_dtype == ME_F32, "bad second-moment dtype");
     AdamArgs a{};
@@ -1624,6 +1644,7 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
     a.param_bf16 = param_dtype == ME_BF16;
     a.rowwise = rowwise != 0;
     a.sq_bf16 = !rowwise && sq_dtype == ME_BF16;
+    a.grad_bf16 = grad_dtype == ME_BF16;
     a.sr = stochastic_rounding != 0;
     a.lazy = lazy != 0;
     a.seed = seed;
@@ -1651,7 +1672,7 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
             t.exp_avg = static_cast<uint8_t *>(exp_avgs[k]);
             t.exp_avg_sq = static_cast<uint8_t *>(exp_avg_sqs[k]);
             t.rows = rows[k];
-            t.grads = grads[k];
+            t.grads = static_cast<const uint8_t *>(grads[k]);
             t.n = n_rows[k];
             t.first = total;
             const double step = static_cast<double>(steps[k]);
@@ -1699,22 +1720,18 @@ extern "C" int me_sparse_adam(int32_t n_tables, void *const *params, void *const
                           }();
         if (wide) {
             const dim3 grid(static_cast<unsigned>(ceil_div(total, kThreads / 64)));
-            if (a.param_bf16 && a.rowwise)
-                hipLaunchKernelGGL((adam_rows_wide<8, true, true>), grid, dim3(kThreads), 0, s, a);
-            else if (a.param_bf16)
-                hipLaunchKernelGGL((adam_rows_wide<8, true, false>), grid, dim3(kThreads), 0, s, a);
-            else if (a.rowwise)
-                hipLaunchKernelGGL((adam_rows_wide<8, false, true>), grid, dim3(kThreads), 0, s, a);
+            if (a.grad_bf16)
+                launch_adam_wide<true>(a.param_bf16 != 0, a.rowwise != 0, grid, s, a);
             else
-                hipLaunchKernelGGL((adam_rows_wide<8, false, false>), grid, dim3(kThreads), 0, s, a);
+                launch_adam_wide<false>(a.param_bf16 != 0, a.rowwise != 0, grid, s, a);
         } else if (lpr8 || lpr4) {
             const int lpr = lpr8 ? lpr8 : lpr4;
             const int64_t per_block = (64 / lpr) * (kThreads / 64);
             const dim3 grid(static_cast<unsigned>(ceil_div(total, per_block)));
             if (lpr8)
-                launch_adam_vec<8>(lpr, a.param_bf16 != 0, a.rowwise != 0, grid, s, a);
+                launch_adam_vec<8>(lpr, a.param_bf16 != 0, a.rowwise != 0, a.grad_bf16 != 0, grid, s, a);
             else
-                launch_adam_vec<4>(lpr, a.param_bf16 != 0, a.rowwise != 0, grid, s, a);
+                launch_adam_vec<4>(lpr, a.param_bf16 != 0, a.rowwise != 0, a.grad_bf16 != 0, grid, s, a);
         } else {
             const dim3 grid(static_cast<unsigned>(ceil_div(total, kThreads / 64)));
             hipLaunchKernelGGL(adam_rows, grid, dim3(kThreads), 0, s, a);

@@ -827,7 +827,7 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
     """One LazyAdamW step on the given rows of each table (micro_engram/optim.py:65-133), all
     tables in one launch. params/exp_avgs [rows_k, D]; exp_avg_sqs [rows_k] fp32 (row-wise) or
     like params; rows int64 [n_k] unique; grads fp32 [n_k, D]; steps: step counts after the
-    increment. Updates the tensors in place."""
+    increment. grads fp32, or all bf16. Updates the tensors in place."""
     dev = require_gpu(*params, *exp_avgs, *exp_avg_sqs, *rows, *grads)
     n = len(params)
     if not (len(exp_avgs) == len(exp_avg_sqs) == len(rows) == len(grads) == len(steps) == n):
@@ -837,6 +837,7 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
     dim = params[0].shape[1]
     pdt = params[0].dtype
     f32, i64 = torch.float32, torch.int64
+    gdt = grads[0].dtype if grads[0].dtype in (f32, torch.bfloat16) else f32
     # one pass: check every table's tensors (the kernel trusts these shapes) and collect the
     # pointers; rows and grads that are not contiguous are copied (kept alive in `held`)
     held, pp, mp, vp, rp, gp, counts = [], [], [], [], [], [], []
@@ -850,8 +851,9 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
                 or (rowwise and v.dtype != f32)):
             raise ValueError("[micro_engram] sparse_adam: exp_avg_sq has the wrong shape or dtype")
         k = r.numel()
-        if r.dtype != i64 or g.dtype != f32 or g.shape != (k, dim):
-            raise ValueError("[micro_engram] sparse_adam: rows must be int64 [n], grads fp32 [n, D]")
+        if r.dtype != i64 or g.dtype != gdt or g.shape != (k, dim):
+            raise ValueError("[micro_engram] sparse_adam: rows must be int64 [n], grads fp32 (or all "
+                             "bf16) [n, D]")
         if not r.is_contiguous():
             r = r.contiguous()
             held.append(r)
@@ -868,18 +870,23 @@ def sparse_adam(params, exp_avgs, exp_avg_sqs, rows, grads, steps, stream_ids, *
     sparse_adam_launch(dev, ptr_array(pp), ptr_array(mp), ptr_array(vp), n, dim, dtype_code(params[0]),
                        sq_code, ptr_array(rp), ptr_array(gp), i64_array(counts), steps, stream_ids,
                        lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, rowwise=rowwise, lazy=lazy,
-                       stochastic_rounding=stochastic_rounding, seed=seed)
+                       stochastic_rounding=stochastic_rounding, seed=seed, grad_dtype=dtype_code(grads[0]))
 
 
 def sparse_adam_launch(dev, param_ptrs, exp_avg_ptrs, exp_avg_sq_ptrs, n, dim, dtype, sq_dtype,
                        row_ptrs, grad_ptrs, counts, steps, stream_ids, *, lr, betas, eps, weight_decay,
-                       rowwise, lazy, stochastic_rounding, seed):
+                       rowwise, lazy, stochastic_rounding, seed, grad_dtype=ME_F32):
     """The launch of sparse_adam from pointer arrays (ctypes) that a caller has already checked
     against the tensors' shapes: n tables of [rows, dim] elements of `dtype`, their moments, and
-    for each its `counts[k]` unique int64 rows and fp32 [counts[k], dim] gradient rows. For callers
-    that keep the arrays of tensors which stay put between steps (the optimizer)."""
-    call("me_sparse_adam", n, param_ptrs, exp_avg_ptrs, exp_avg_sq_ptrs, row_ptrs, grad_ptrs, counts,
-         i64_array([int(s) for s in steps]), i32_array([int(s) for s in stream_ids]), dim, dtype,
+    for each its `counts[k]` unique int64 rows and [counts[k], dim] gradient rows of grad_dtype
+    (ME_F32 or ME_BF16); steps and stream_ids as lists or ready ctypes arrays. For callers that
+    keep the arrays of tensors which stay put between steps (the optimizer)."""
+    if not isinstance(steps, ctypes.Array):
+        steps = i64_array([int(s) for s in steps])
+    if not isinstance(stream_ids, ctypes.Array):
+        stream_ids = i32_array([int(s) for s in stream_ids])
+    call("me_sparse_adam", n, param_ptrs, exp_avg_ptrs, exp_avg_sq_ptrs, row_ptrs, grad_ptrs, grad_dtype, counts,
+         steps, stream_ids, dim, dtype,
          int(bool(rowwise)), sq_dtype, int(bool(lazy)), float(lr), float(betas[0]), float(betas[1]),
          float(eps), float(weight_decay), int(bool(stochastic_rounding)), int(seed) & ((1 << 64) - 1),
          stream_of(dev))

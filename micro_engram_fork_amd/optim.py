@@ -151,7 +151,8 @@ class LazyAdamW(torch.optim.Optimizer):
         for (device, dtype, dim, rowwise, lazy, vdtype), b in batches.items():
             b.update(device=device, dim=dim, dtype=ops.dtype_code(torch.empty(0, dtype=dtype)), rowwise=rowwise, lazy=lazy,
                      sq_dtype=ops.ME_F32 if rowwise else ops.dtype_code(torch.empty(0, dtype=vdtype)),
-                     P_arr=ops.ptr_array(b["P"]), M_arr=ops.ptr_array(b["M"]), V_arr=ops.ptr_array(b["V"]))
+                     P_arr=ops.ptr_array(b["P"]), M_arr=ops.ptr_array(b["M"]), V_arr=ops.ptr_array(b["V"]),
+                     stream_arr=ops.i32_array(b["stream_ids"]))
         plan = plans[gi] = {"key": key, "members": members, "batches": list(batches.values())}
         return plan
 
@@ -193,6 +194,10 @@ class LazyAdamW(torch.optim.Optimizer):
         batch, ks = SparseBatch.common(members)
         if batch is None:
             return None
+        return LazyAdamW._batch_pointers_of(b, batch, ks, step_of)
+
+    @staticmethod
+    def _batch_pointers_of(b, batch, ks, step_of):
         rows, sums = batch.rows, batch.sums
         if (rows.dtype != torch.int64 or sums.dtype != torch.float32 or not rows.is_contiguous()
                 or not sums.is_contiguous() or sums.dim() != 2 or sums.shape[1] != b["dim"]
@@ -244,6 +249,47 @@ class LazyAdamW(torch.optim.Optimizer):
                     p.grad = None
 
     @torch.no_grad()
+    def prepare_step(self):
+        """Builds ahead of time the launch arguments of the next step for the batches whose
+        members' sparse gradients are all slices of one row-lookup backward (SparseBatch), so
+        that step() only checks that nothing changed -- the same batch, the same step counts --
+        and launches. Meant for the time between the backward and a host sync (RowTables.clip
+        calls it before it reads the norm): this host work then overlaps the GPU's backward
+        instead of following the sync. Without a step() after it, it changes nothing."""
+        prepared = {}
+        for gi, group in enumerate(self.param_groups):
+            if not group["lazy"]:
+                continue
+            live = [p for p in group["params"]
+                    if p.grad is not None or getattr(p, "sparse_grad", None) is not None]
+            if not live or any(not self.state[p] for p in live):
+                continue
+            nxt = [float(self.state[p]["step"]) + 1 for p in live]
+            plan = self._launch_plan(gi, group, live)
+            for bi, b in enumerate(plan["batches"]):
+                batch, ks = SparseBatch.common([live[i] for i in b["pos"]])
+                if batch is None:
+                    continue
+                fast = self._batch_pointers_of(b, batch, ks, nxt)
+                if fast is None:
+                    continue
+                held, rp, gp, counts, steps = fast
+                prepared[(gi, bi)] = (batch, ks, held, steps, ops.ptr_array(rp), ops.ptr_array(gp),
+                                      ops.i64_array(counts), ops.i64_array(steps))
+        self._prepared = prepared
+
+    def _prepared_launch(self, gi, bi, b, live, step_of):
+        """The arrays prepare_step built for batch bi of group gi, if they still hold."""
+        prepared = self.__dict__.get("_prepared")
+        pre = prepared.pop((gi, bi), None) if prepared else None
+        if pre is None:
+            return None
+        batch, ks = SparseBatch.common([live[i] for i in b["pos"]])
+        if batch is not pre[0] or ks != pre[1] or [int(step_of[i]) for i in b["pos"]] != pre[3]:
+            return None
+        return pre
+
+    @torch.no_grad()
     def _step(self, closure=None):
         loss = None
         if closure is not None:
@@ -259,11 +305,30 @@ class LazyAdamW(torch.optim.Optimizer):
                     self.init_state(self.state[p], p, group)
             step_of = self._advance_steps(gi, group, live)
             plan = self._launch_plan(gi, group, live)
-            for b in plan["batches"]:
+            for bi, b in enumerate(plan["batches"]):
+                pre = self._prepared_launch(gi, bi, b, live, step_of) if group["lazy"] else None
+                if pre is not None:  # arguments built by prepare_step while the GPU was busy
+                    ops.sparse_adam_launch(b["device"], b["P_arr"], b["M_arr"], b["V_arr"], len(pre[3]),
+                                           b["dim"], b["dtype"], b["sq_dtype"], pre[4], pre[5], pre[6], pre[7],
+                                           b["stream_arr"], lr=group["lr"], betas=group["betas"],
+                                           eps=group["eps"], weight_decay=group["weight_decay"],
+                                           rowwise=b["rowwise"], lazy=b["lazy"],
+                                           stochastic_rounding=group.get("stochastic_rounding", True),
+                                           seed=self.seed)
+                    torch.autograd.graph.increment_version(b["written"])
+                    continue
                 dim, held, rp, gp, counts, steps = b["dim"], [], [], [], [], []
                 fast = self._batch_pointers(b, live, step_of) if group["lazy"] else None
                 if fast is not None:
                     held, rp, gp, counts, steps = fast
+                # gradients go to the kernel as they are when all are fp32 or all bf16 (it reads
+                # either), else as fp32 copies
+                grad_dtype = torch.float32
+                if fast is None:
+                    dts = {(p.sparse_grad[1] if getattr(p, "sparse_grad", None) is not None else p.grad).dtype
+                           for p in (live[i] for i in b["pos"])}
+                    if dts == {torch.bfloat16}:
+                        grad_dtype = torch.bfloat16
                 for j, i in enumerate(b["pos"] if fast is None else ()):
                     p = live[i]
                     sparse = getattr(p, "sparse_grad", None)
@@ -272,9 +337,9 @@ class LazyAdamW(torch.optim.Optimizer):
                             raise ValueError("sparse row gradients need lazy=True")
                         rows, g = sparse
                         rows = rows if rows.dtype == torch.int64 else rows.long()
-                        g = g if g.dtype == torch.float32 else g.float()
+                        g = g if g.dtype == grad_dtype else g.float()
                     else:
-                        g = p.grad if p.grad.dtype == torch.float32 else p.grad.float()
+                        g = p.grad if p.grad.dtype == grad_dtype else p.grad.float()
                         rows = b["arange"][j]
                         n = p.shape[0] if p.dim() >= 1 else 1
                         if rows is None or rows.numel() != n or rows.device != p.device:
@@ -297,10 +362,11 @@ class LazyAdamW(torch.optim.Optimizer):
                     steps.append(int(step_of[i]))
                 ops.sparse_adam_launch(b["device"], b["P_arr"], b["M_arr"], b["V_arr"], len(rp), dim,
                                        b["dtype"], b["sq_dtype"], ops.ptr_array(rp), ops.ptr_array(gp),
-                                       ops.i64_array(counts), steps, b["stream_ids"], lr=group["lr"],
+                                       ops.i64_array(counts), steps, b["stream_arr"], lr=group["lr"],
                                        betas=group["betas"], eps=group["eps"],
                                        weight_decay=group["weight_decay"], rowwise=b["rowwise"], lazy=b["lazy"],
-                                       stochastic_rounding=group.get("stochastic_rounding", True), seed=self.seed)
+                                       stochastic_rounding=group.get("stochastic_rounding", True), seed=self.seed,
+                                       grad_dtype=ops.ME_BF16 if grad_dtype == torch.bfloat16 else ops.ME_F32)
                 # the kernel wrote through raw pointers: move the version counters as torch's
                 # own in-place ops would (autograd's saved-tensor checks and caches keyed on
                 # them then see the update) (p itself: p.data has a version counter of its own)

@@ -293,6 +293,8 @@ class RowTables:
             ops.sumsq(span, sq, accumulate=True)
             if max_norm and max_norm > 0:
                 ops.clip_scale(span, sq, max_norm)
+            if self.optimizer is not None:
+                self.optimizer.prepare_step()  # host work of the next step, before the host read
             self.last_grad_norm = float(sq.sqrt().item())
             return self.last_grad_norm
         squares, scaled = [], []

@@ -662,3 +662,29 @@ def test_training_step_fast_paths_equal_the_general_ones():
     assert fast_norms == gen_norms
     for (p1, m1, v1, s1), (p2, m2, v2, s2) in zip(fast, general):
         assert torch.equal(p1, p2) and torch.equal(m1, m2) and torch.equal(v1, v2) and s1 == s2 == 3.0
+
+
+@pytest.mark.parametrize("D,rowwise,lazy", [(1536, False, False), (1536, True, True), (64, True, True),
+                                            (64, False, False), (12, False, True), (3, True, False)])
+def test_sparse_adam_reads_bf16_gradients_as_their_fp32_values(D, rowwise, lazy):
+    # bf16 gradient rows (the dense weights' autograd gradients) go to the kernel as they are:
+    # the update equals the one from their fp32 copies bit for bit, on the wide (1536 columns),
+    # vector (64, 12) and generic (3) kernels
+    g = torch.Generator().manual_seed(D)
+    R, n = 200, 90
+    init = (torch.randn(R, D, generator=g) * 0.02).bfloat16().to(DEV)
+    rows = torch.randperm(R, generator=g)[:n].sort().values.to(DEV)
+    grads = (torch.randn(n, D, generator=g) * 1e-3).bfloat16().to(DEV)
+    grads[::5] = 0
+    outs = []
+    for gr in (grads, grads.float()):
+        p, m = init.clone(), (init * 0.1).clone()
+        v = torch.full((R,), 1e-6, device=DEV) if rowwise else (init.float() ** 2).bfloat16()
+        for step in (1, 2):
+            ops.sparse_adam([p], [m], [v], [rows], [gr], [step], [5], lr=5e-3, betas=(0.9, 0.999),
+                            eps=1e-8, weight_decay=0.01, rowwise=rowwise, lazy=lazy,
+                            stochastic_rounding=True, seed=77)
+        outs.append((p, m, v))
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b)
