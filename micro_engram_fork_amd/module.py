@@ -56,20 +56,40 @@ class _RowIds(list):
     """The per-table row ids hash_ids / hash_prev return (a list of n_tables tensors, as the
     reference's), which are the rows of one [n_tables, N] tensor: it remembers that tensor, so
     the lookup can take it as it is while the list and the tensor are unchanged (the same
-    element objects, no in-place write since: the views share the tensor's version counter)."""
+    element objects, no in-place write since: the views share the tensor's version counter).
+    From hash_prev without gradients it also carries the rows read with the ids."""
 
-    __slots__ = ("stacked", "views", "version")
+    __slots__ = ("stacked", "views", "version", "rows")
 
-    def __init__(self, stacked):
+    def __init__(self, stacked, rows=None):
         views = stacked.unbind(0)
         super().__init__(views)
         self.views = views
         self.stacked = stacked.reshape(len(views), -1)
-        self.version = stacked._version
+        self.version = _version_of(stacked)
+        self.rows = rows  # (memory vectors, their version, the tables' key) read with the ids
+
+    def rows_for(self, tables):
+        """The memory vectors read together with these ids, while the ids, the vectors and the
+        tables (address, shape and version counter of each) are all as they were then."""
+        rows = self.rows
+        if (rows is None or not self.unchanged() or _version_of(rows[0]) != rows[1]
+                or rows[2] != _tables_key(tables)):
+            return None
+        return rows[0]
 
     def unchanged(self):
-        return (len(self) == len(self.views) and self.stacked._version == self.version
+        return (len(self) == len(self.views) and _version_of(self.stacked) == self.version
                 and all(a is b for a, b in zip(self, self.views)))
+
+
+def _version_of(t):
+    """A tensor's version counter; None for an inference tensor, which keeps none."""
+    return None if t.is_inference() else t._version
+
+
+def _tables_key(tables):
+    return tuple((t.data_ptr(), t.shape, _version_of(t)) for t in tables)
 
 
 class _GateResidual(torch.autograd.Function):
@@ -308,11 +328,33 @@ class MicroEngram(nn.Module):
 
     def hash_prev(self, ids):
         """Row ids from [N, W] ids of each token and its predecessors, -1 where missing: list of
-        n_tables LongTensors [N] (module.py:207-226)."""
+        n_tables LongTensors [N] (module.py:207-226).
+
+        Without gradients (serving) the rows are read in the same launch (me_hash_prev_gather:
+        one kernel where hashing and gathering apart take two) and travel with the returned list,
+        so that the next inject on it reads no rows again -- while the list, the tables and (for
+        tensors made outside inference mode) the ids and rows are unchanged: version counters
+        see in-place writes through the tensors, the optimizers' updates included, not writes
+        through .data; ids made under inference_mode keep no counter, so an in-place write to
+        them before the inject is not seen. lookup hands the rows out and drops them."""
         canon, mults, ident = self._hash_consts(ids.device)
+        if not torch.compiler.is_compiling() and self._reads_rows_with_ids():
+            tables = self._table_weights()
+            key = _tables_key(tables)
+            if all(k[2] is not None for k in key):
+                mem, idx = ops.hash_prev_gather(ids, canon, mults, self._table_orders, self.table_rows,
+                                                int(self.pad_id), tables, True, ident)
+                return _RowIds(idx, (mem, _version_of(mem), key))
         idx = ops.hash_prev(ids, canon, mults, self._table_orders, self.table_rows,
                             int(self.pad_id), ident)
         return list(idx.unbind(0)) if torch.compiler.is_compiling() else _RowIds(idx)
+
+    def _reads_rows_with_ids(self):
+        """Whether hash_prev reads the rows with the ids: no gradients, the module's own lookup,
+        tables of this module (not a row server's)."""
+        return (not torch.is_grad_enabled() and not self._lookup_replaced()
+                and not (self.row_lookup_fn is not None and self.row_shards is not None)
+                and (self.row_shards is not None or "tables" in self._modules))
 
     # -------------------------------------------------------------------------------- lookup
     @staticmethod
@@ -348,10 +390,17 @@ class MicroEngram(nn.Module):
             return memory(self, idx)
         return torch.cat(fn(self, idx), dim=-1).reshape(idx[0].numel(), -1)
 
-    def _mem(self, idx):
+    def _mem(self, idx, hand_out=False):
         if self.row_lookup_fn is not None and self.row_shards is not None:
             return self._served_memory(idx)
-        return ops.gather(self._stacked_idx(idx), self._table_weights())
+        tables = self._table_weights()
+        if isinstance(idx, _RowIds) and idx.rows is not None:
+            mem = idx.rows_for(tables)
+            if hand_out:  # views of the rows leave the module: no later read may trust them
+                idx.rows = None
+            if mem is not None:  # read together with the ids by hash_prev
+                return mem
+        return ops.gather(self._stacked_idx(idx), tables)
 
     def _mem_grad(self, idx):
         """The memory vectors [N, n_tables * D] with the tables' gradients attached: the row
@@ -387,7 +436,7 @@ class MicroEngram(nn.Module):
         if torch.is_grad_enabled() and any(t.weight.requires_grad for t in self.tables):
             mem = self._mem_grad(idx)
         else:
-            mem = self._mem(idx)
+            mem = self._mem(idx, hand_out=True)
         D = self.engram_dim
         return [mem[:, k * D:(k + 1) * D].reshape(*shape, D) for k in range(len(idx))]
 

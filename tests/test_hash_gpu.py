@@ -104,7 +104,7 @@ def test_lookup_rows_bit_exact(dtype, dim):
     rows = eng.lookup(idx)
     tables = [t.weight.detach().cpu().float().numpy() for t in eng.tables]
     want = oracle.lookup(tables, [i.cpu().numpy() for i in idx])
-    got = torch.cat([r.reshape(-1, dim) for r in rows], dim=-1).float().cpu().numpy()
+    got = torch.cat([r.detach().reshape(-1, dim) for r in rows], dim=-1).float().cpu().numpy()
     assert np.array_equal(got, want)
     assert rows[0].shape == (4, 33, dim)
 
@@ -113,7 +113,7 @@ def test_lookup_out_of_range_rows_are_zero():
     # the masked serving lookup (micro_engram_vllm/tp.py:20-39 at TP=1): rows outside a table
     eng = _engram(dim=8, sizes={2: 10, 3: 20})
     idx = [torch.tensor([0, 9, 10, -1, 5], device=DEV)] * 2 + [torch.tensor([19, 20, 3, -7, 0], device=DEV)] * 2
-    got = torch.cat(eng.lookup(idx), dim=-1).cpu().numpy()
+    got = torch.cat(eng.lookup(idx), dim=-1).detach().cpu().numpy()
     tables = [t.weight.detach().cpu().numpy() for t in eng.tables]
     assert np.array_equal(got, oracle.lookup(tables, [i.cpu().numpy() for i in idx]))
 
