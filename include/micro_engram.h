@@ -351,6 +351,36 @@ int me_dedup_table_bounds(const int64_t *uniq, int64_t n, const int64_t *count,
                           int64_t *info, void *stream);
 
 /*
+ * me_dedup_tables -- the key half of a row lookup's dedup from its per-table row ids, and the
+ * tables' bounds in it: what me_dedup_keys + me_dedup_table_bounds give for the token-major keys
+ * offset_k + idx[k][t] (lookup position t * n_tables + k), in two launches for up to 16,384
+ * tokens (micro_engram/rows.py:81 torch.unique(return_inverse=True) over the lookups' keys, and
+ * the per-table slices of rows.py:123-129). Every table holds n lookups, so table k's part of the
+ * sorted order is [k * n, (k + 1) * n): each workgroup takes one range of one table's rows, reads
+ * the table's ids, and sorts its lookups where they land; a second launch numbers the unique keys.
+ * Larger n: the keys, then the me_dedup_keys path and the bounds.
+ *
+ *   idx          [n_tables, idx_table_stride] int64 row ids (token t of table k at
+ *                idx[k * idx_table_stride + t]); rows outside [0, table_rows[k]) are outside the
+ *                contract (clamped, so nothing is written out of bounds)
+ *   table_rows   n_tables host int64 row counts; offset_k = sum of the rows of tables below k
+ *   uniq         [n * n_tables] int64 unique keys ascending (the first count are valid)
+ *   local_rows   [n * n_tables] int64 row of each unique key in its table
+ *   inv          [n * n_tables] int64 unique index of each lookup position, or null: not
+ *                written (me_dedup_sums reads the plan only)
+ *   info         [n_tables + 2] int64: count, the first unique index of each table, count
+ *   plan         at least me_dedup_plan_size(n * n_tables) bytes, read by me_dedup_sums with
+ *                count = info
+ *   workspace    at least me_dedup_tables_workspace_size bytes (free again when the work ends)
+ */
+int me_dedup_tables_workspace_size(int64_t n, int32_t n_tables, const int64_t *table_rows,
+                                   size_t *bytes);
+int me_dedup_tables(const int64_t *idx, int64_t idx_table_stride, int64_t n, int32_t n_tables,
+                    const int64_t *table_rows, int64_t *uniq, int64_t *local_rows, int64_t *inv,
+                    int64_t *info, void *plan, size_t plan_size, void *workspace,
+                    size_t workspace_size, void *stream);
+
+/*
  * me_dedup_plan_size -- bytes of the segment plan me_dedup_keys writes for n keys.
  */
 int me_dedup_plan_size(int64_t n, size_t *bytes);

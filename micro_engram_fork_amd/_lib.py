@@ -52,6 +52,9 @@ SIGNATURES = {
     "me_dedup_plan_size": [c_i64, ctypes.POINTER(c_size)],
     "me_dedup_keys": [c_ptr, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_size, c_ptr, c_size, c_ptr],
     "me_dedup_table_bounds": [c_ptr, c_i64, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr],
+    "me_dedup_tables_workspace_size": [c_i64, c_i32, c_ptr, ctypes.POINTER(c_size)],
+    "me_dedup_tables": [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_size,
+                        c_ptr, c_size, c_ptr],
     "me_dedup_sums": [c_ptr, c_size, c_i64, c_ptr, c_ptr, c_int, c_i32, c_ptr, c_ptr],
     "me_sumsq": [c_ptr, c_i64, c_ptr, c_int, c_ptr, c_size, c_ptr],
     "me_sparse_adam": [c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_int, c_ptr, c_ptr, c_ptr, c_i32, c_int,

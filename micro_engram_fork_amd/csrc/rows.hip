@@ -665,7 +665,14 @@ __global__ __launch_bounds__(kThreads) void gd_emit(const uint64_t *comp, const 
         *count = static_cast<int64_t>(total);
         seg_start[total] = lo + size;
     }
-    auto item = [&](uint32_t i) { return in_lds ? s_c[i] : sorted[i]; };
+    // LDS and global memory through their own address spaces: one generic pointer for both would
+    // compile to flat loads, whose aperture check sees the base before the instruction offset
+    gmem_ptr<const uint64_t> gsorted = as_global(sorted);
+    auto item = [&](uint32_t i) {
+        uint64_t v;
+        if (in_lds) v = s_c[i]; else v = gsorted[i];
+        return v;
+    };
     for (uint32_t c0 = 0; c0 < size; c0 += kThreads * kItems) {
         const uint32_t i0 = c0 + static_cast<uint32_t>(tid) * kItems;
         uint64_t v[kItems];
@@ -699,6 +706,326 @@ __global__ __launch_bounds__(kThreads) void gd_emit(const uint64_t *comp, const 
         }
         run += chunk_heads;
     }
+}
+
+// ---- table dedup ------------------------------------------------------------------------------
+// The key half of a row lookup's dedup when its keys come as per-table row ids: idx[k * stride +
+// t] is the row of token t in table k (t < n), the key is offset_k + row and the lookup's
+// position is t * nt + k (the token-major order of the gradient rows). Every table holds exactly
+// n lookups, so in sorted key order table k's lookups fill [k * n, (k + 1) * n). Table k's rows
+// are split into parts of 2^shift_k rows (part = row >> shift_k), and a part's place inside its
+// table is the number of the table's lookups in lower parts -- which the part's workgroup counts
+// itself while it reads the table's ids. So every part sorts its lookups where they land, with no
+// exchange between workgroups; only the unique numbering needs the earlier parts' unique counts,
+// which is the second launch:
+//   td_part  per (table, part): the table's ids read once (two per thread per round of 512
+//            tokens, kept in registers), the part's (row, token) composites compacted in token
+//            order into LDS (wave ballots, then one scan of the per-(round, wave) counts), ranked
+//            inside 1024 buckets of their top row bits, and written at the part's place: spos
+//            (the position) and srow (the row); its size, place and unique count into gsize,
+//            gstart and ucount. A part larger than LDS sorts in global memory (stable LSD radix).
+//   td_emit  per (table, part): its unique keys numbered after the earlier parts' (a block sum
+//            of their unique counts), then uniq, local rows, inv, the segment plan and the
+//            table bounds (info = [count, first unique index of each table, count]).
+constexpr uint32_t kTdMaxN = 16384;           // tokens per table this path takes
+constexpr int kTdRounds = kTdMaxN / (2 * kThreads);
+constexpr int kTdCap = 2048;                  // composites a part sorts in LDS
+constexpr int kTdBucketBits = 10;
+constexpr int kTdBuckets = 1 << kTdBucketBits;
+constexpr int kTdPartTarget = 512;            // lookups per part aimed at
+
+struct TdArgs {
+    const int64_t *idx;
+    int64_t stride;
+    uint32_t n;
+    int nt;
+    uint32_t ngroups;
+    int64_t rows[ME_MAX_TABLES];
+    int64_t off[ME_MAX_TABLES];           // key offset of table k
+    int32_t shift[ME_MAX_TABLES];         // log2 of a part's rows
+    uint32_t gbase[ME_MAX_TABLES + 1];    // first part (group) of table k; gbase[nt] = ngroups
+    uint32_t *spos, *seg_start, *seg_pos;  // the plan
+    uint32_t *srow;                        // [n * nt] row of each lookup in sorted order (parts
+                                           // larger than LDS)
+    uint64_t *slot;                        // [ngroups * kTdCap] a part's sorted (position << 32 |
+                                           // row), at a place known before the part's size
+    uint64_t *tmp_a, *tmp_b;               // [n * nt] each: parts larger than LDS
+    uint32_t *gstart, *gsize, *ucount;     // [ngroups]
+    int64_t *uniq, *local, *inv, *info;
+};
+
+__device__ __forceinline__ int td_table_of(const TdArgs &a, uint32_t g) {
+    int k = 0;
+    while (k + 1 < a.nt && a.gbase[k + 1] <= g) ++k;
+    return k;
+}
+
+// kRounds: rounds of 512 tokens the part's workgroup reads (a power of two, >= the table's n /
+// 512); kVec2: two ids per 16-byte load (ids 16-byte aligned, stride and n even).
+template <int kRounds, bool kVec2>
+__global__ __launch_bounds__(kThreads) void td_part(const TdArgs a) {
+    __shared__ uint64_t s_a[kTdCap];
+    __shared__ uint64_t s_b[kTdCap];
+    __shared__ uint32_t s_sb[kTdBuckets + 1];  // bucket starts
+    __shared__ uint32_t s_cur[kTdBuckets];     // bucket fill counters
+    __shared__ uint32_t s_wtot[kThreads / 64];
+    __shared__ uint32_t s_red[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t g = blockIdx.x;
+    const int k = td_table_of(a, g);
+    const uint32_t part = g - a.gbase[k];
+    const int sh = a.shift[k];
+    const int64_t rmax = a.rows[k] - 1;
+    const uint32_t n = a.n;
+    const int64_t *ids = a.idx + static_cast<int64_t>(k) * a.stride;
+
+    // ---- the table's ids: token t = r * 512 + 2 * tid + h, every load in flight at once. Rows
+    // outside [0, rows) (outside the contract) are clamped, so nothing lands out of bounds.
+    int64_t v[kRounds][2];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+        const uint32_t t0 = static_cast<uint32_t>(r * 2 * kThreads + 2 * tid);
+        if (kVec2) {
+            u32x4_v w = u32x4_v{0u, 0u, 0u, 0u};
+            if (t0 < n) w = *as_global(reinterpret_cast<const u32x4_v *>(ids + t0));
+            v[r][0] = static_cast<int64_t>((static_cast<uint64_t>(w[1]) << 32) | w[0]);
+            v[r][1] = static_cast<int64_t>((static_cast<uint64_t>(w[3]) << 32) | w[2]);
+        } else {
+            v[r][0] = t0 < n ? ids[t0] : 0;
+            v[r][1] = t0 + 1 < n ? ids[t0 + 1] : 0;
+        }
+    }
+    // bit 2r + h of `match`: a lookup of this part; counts of this part's and of lower parts'
+    uint32_t row[kRounds][2];
+    uint64_t match = 0;
+    uint32_t cm = 0, cl = 0;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t t = static_cast<uint32_t>(r * 2 * kThreads + 2 * tid + h);
+            const int64_t x = v[r][h];
+            row[r][h] = static_cast<uint32_t>(x < 0 ? 0 : (x > rmax ? rmax : x));
+            const uint32_t p = row[r][h] >> sh;
+            const bool valid = t < n;
+            const bool m = valid && p == part;
+            cm += m ? 1u : 0u;
+            cl += (valid && p < part) ? 1u : 0u;
+            match |= m ? (1ull << (2 * r + h)) : 0ull;
+        }
+    }
+    // both counts in one block scan (each below 2^16: at most n <= 16384 of either); the low half
+    // of this thread's exclusive prefix is where its own lookups of the part go
+    uint32_t tot;
+    const uint32_t pre = block_exclusive_scan((cl << 16) | cm, s_wtot, &tot);
+    const uint32_t m = tot & 0xffffu;
+    const uint32_t start = static_cast<uint32_t>(k) * n + (tot >> 16);
+    const bool in_lds = m <= static_cast<uint32_t>(kTdCap);
+    uint64_t *gbuf = a.tmp_a + start;
+    // ---- the part's composites (row in part << 32 | token), each thread's at its own slots, in
+    // no particular order (the sort below orders whole composites)
+    const uint32_t lmask = (1u << sh) - 1u;
+    uint32_t dst = pre & 0xffffu;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if ((match >> (2 * r + h)) & 1ull) {
+                const uint32_t t = static_cast<uint32_t>(r * 2 * kThreads + 2 * tid + h);
+                const uint64_t c = (static_cast<uint64_t>(row[r][h] & lmask) << 32) | t;
+                if (in_lds) s_a[dst] = c; else gbuf[dst] = c;
+                ++dst;
+            }
+        }
+    }
+    __syncthreads();
+    if (in_lds) {
+        // buckets of the top row bits, then each composite ranked inside its bucket (composites
+        // are distinct: the order of (row, token), i.e. the stable order of the keys)
+        const int bbits = sh < kTdBucketBits ? sh : kTdBucketBits;
+        const int bsh = 32 + sh - bbits;
+        const uint32_t bmask = (1u << bbits) - 1u;
+        auto bucket = [&](uint64_t c) { return static_cast<uint32_t>(c >> bsh) & bmask; };
+        constexpr int kPer = kTdBuckets / kThreads;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) s_cur[tid * kPer + q] = 0u;
+        __syncthreads();
+        for (uint32_t i = tid; i < m; i += kThreads) atomicAdd(&s_cur[bucket(s_a[i])], 1u);
+        __syncthreads();
+        {
+            uint32_t c[kPer], sum = 0;
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                c[q] = s_cur[tid * kPer + q];
+                sum += c[q];
+            }
+            uint32_t btot;
+            uint32_t st = block_exclusive_scan(sum, s_wtot, &btot);
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                s_sb[tid * kPer + q] = st;
+                s_cur[tid * kPer + q] = st;
+                st += c[q];
+            }
+            if (tid == 0) s_sb[kTdBuckets] = m;
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < m; i += kThreads) {
+            const uint64_t c = s_a[i];
+            s_b[atomicAdd(&s_cur[bucket(c)], 1u)] = c;
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < m; i += kThreads) {
+            const uint64_t c = s_b[i];
+            const uint32_t j = bucket(c);
+            const uint32_t blo = s_sb[j], bhi = s_sb[j + 1];
+            uint32_t rank = 0;
+            uint32_t q = blo;
+            for (; q + 8 <= bhi; q += 8) {  // a hot row's repeats: eight reads in flight
+                uint64_t d[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d[e] = s_b[q + e];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) rank += d[e] < c ? 1u : 0u;
+            }
+            for (; q < bhi; ++q) rank += s_b[q] < c ? 1u : 0u;
+            s_a[blo + rank] = c;
+        }
+        __syncthreads();
+    } else {
+        wg_radix_sort(gbuf, a.tmp_b + start, m, 32 + sh);
+    }
+    // ---- the part's lookups at its place: position and row; its unique count. LDS and global
+    // memory are read through their own pointers: a generic pointer into LDS let the compiler
+    // form sorted + i - 1 as an address below the LDS aperture (s_a sits at LDS offset 0) with
+    // the 8 bytes in the instruction offset, and the aperture is checked on that base.
+    uint32_t heads = 0;
+    const uint32_t rbase = part << sh;
+    uint64_t *slot = a.slot + static_cast<uint64_t>(g) * kTdCap;
+    auto put = [&](uint32_t i, uint64_t c, uint64_t prev) {
+        const uint32_t rl = static_cast<uint32_t>(c >> 32), t = static_cast<uint32_t>(c);
+        heads += (i == 0 || static_cast<uint32_t>(prev >> 32) != rl) ? 1u : 0u;
+        const uint32_t pos = t * static_cast<uint32_t>(a.nt) + static_cast<uint32_t>(k);
+        a.spos[start + i] = pos;
+        if (in_lds) slot[i] = (static_cast<uint64_t>(pos) << 32) | (rbase + rl);
+        else a.srow[start + i] = rbase + rl;
+    };
+    if (in_lds) {
+        for (uint32_t i = tid; i < m; i += kThreads) put(i, s_a[i], s_a[i > 0 ? i - 1 : 0]);
+    } else {
+        gmem_ptr<const uint64_t> gs = as_global(static_cast<const uint64_t *>(gbuf));
+        for (uint32_t i = tid; i < m; i += kThreads) put(i, gs[i], gs[i > 0 ? i - 1 : 0]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) heads += __shfl_xor(heads, o, 64);
+    if (lane == 0) s_red[wave] = heads;
+    __syncthreads();
+    if (tid == 0) {
+        a.gstart[g] = start;
+        a.gsize[g] = m;
+        a.ucount[g] = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void td_emit(const TdArgs a) {
+    __shared__ uint32_t s_wtot[kThreads / 64];
+    const int tid = threadIdx.x;
+    const uint32_t g = blockIdx.x;
+    const int k = td_table_of(a, g);
+    const bool last = g + 1 == a.ngroups;
+    // every first load at once: the part's place and size, the earlier parts' unique counts, and
+    // the part's sorted lookups from its slot (a part that fit LDS left them there; thread tid owns
+    // [8 tid, 8 tid + 8) and reads the one before)
+    const uint32_t lo = a.gstart[g], size = a.gsize[g];
+    const uint64_t *slot = a.slot + static_cast<uint64_t>(g) * kTdCap;
+    uint64_t sv[kItems + 1];
+    sv[0] = tid > 0 ? slot[tid * kItems - 1] : 0ull;
+#pragma unroll
+    for (int e = 0; e < kItems; ++e) sv[e + 1] = slot[tid * kItems + e];
+    const uint32_t lim = last ? a.ngroups : g;
+    uint32_t before = 0, all = 0;
+    for (uint32_t q0 = 0; q0 < lim; q0 += kThreads * 8) {
+        uint32_t c[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t q = q0 + e * kThreads + tid;
+            c[e] = q < lim ? a.ucount[q] : 0u;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t q = q0 + e * kThreads + tid;
+            before += q < g ? c[e] : 0u;
+            all += c[e];
+        }
+    }
+    uint32_t run, total;
+    block_exclusive_scan(before, s_wtot, &run);
+    block_exclusive_scan(all, s_wtot, &total);
+    if (tid == 0) {
+        if (g == a.gbase[k]) a.info[1 + k] = static_cast<int64_t>(run);
+        if (last) {
+            a.info[0] = static_cast<int64_t>(total);
+            a.info[1 + a.nt] = static_cast<int64_t>(total);
+            a.seg_start[total] = a.n * static_cast<uint32_t>(a.nt);
+        }
+    }
+    const int64_t off = a.off[k];
+    const bool from_slot = size <= static_cast<uint32_t>(kTdCap);
+    for (uint32_t c0 = 0; c0 < size; c0 += kThreads * kItems) {
+        const uint32_t i0 = c0 + static_cast<uint32_t>(tid) * kItems;
+        uint32_t r[kItems], p[kItems];
+        uint32_t prev;
+        if (from_slot) {  // one chunk: size <= kTdCap = kThreads * kItems
+            prev = static_cast<uint32_t>(sv[0]);
+#pragma unroll
+            for (int e = 0; e < kItems; ++e) {
+                r[e] = static_cast<uint32_t>(sv[e + 1]);
+                p[e] = static_cast<uint32_t>(sv[e + 1] >> 32);
+            }
+        } else {
+            prev = i0 > 0 && i0 < size ? a.srow[lo + i0 - 1] : 0u;
+#pragma unroll
+            for (int e = 0; e < kItems; ++e) {
+                const uint32_t i = i0 + e;
+                r[e] = i < size ? a.srow[lo + i] : 0u;
+                p[e] = i < size ? a.spos[lo + i] : 0u;
+            }
+        }
+        bool head[kItems];
+        uint32_t nh = 0;
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) {
+            const uint32_t i = i0 + e;
+            head[e] = i < size && (i == 0 || r[e] != prev);
+            nh += head[e] ? 1u : 0u;
+            prev = r[e];
+        }
+        uint32_t chunk_heads;
+        uint32_t u = run + block_exclusive_scan(nh, s_wtot, &chunk_heads);
+#pragma unroll
+        for (int e = 0; e < kItems; ++e) {
+            const uint32_t i = i0 + e;
+            if (i < size) {
+                if (head[e]) {
+                    a.uniq[u] = off + r[e];
+                    a.local[u] = r[e];
+                    a.seg_start[u] = lo + i;
+                    a.seg_pos[u] = p[e];
+                    ++u;
+                }
+                if (a.inv != nullptr) a.inv[p[e]] = static_cast<int64_t>(u) - 1;
+            }
+        }
+        run += chunk_heads;
+    }
+}
+
+// A table's part width: the smallest 2^shift rows for which the table has at most `target`
+// parts (shift <= 31, so a row inside its part fits the 32 bits of a composite).
+int td_shift(int64_t rows, int64_t target) {
+    int s = 0;
+    while (s < 31 && ((rows - 1) >> s) + 1 > target) ++s;
+    return s;
 }
 
 // ---- squared norm ---------------------------------------------------------------------------
@@ -1527,6 +1854,169 @@ extern "C" int me_dedup_table_bounds(const int64_t *uniq, int64_t n, const int64
     hipLaunchKernelGGL(table_bounds_kernel, grid, dim3(kThreads), 0, as_stream(stream), uniq, n, count, t,
                        n_tables, local_rows, info);
     return check_launch("me_dedup_table_bounds");
+}
+
+// ---- the key half from per-table row ids ------------------------------------------------------
+namespace me {
+namespace {
+__global__ __launch_bounds__(kThreads) void td_keys(const TdArgs a, int64_t *keys) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t total = static_cast<int64_t>(a.n) * a.nt;
+    if (i >= total) return;
+    const int64_t t = i / a.nt;
+    const int k = static_cast<int>(i - t * a.nt);
+    const int64_t v = a.idx[static_cast<int64_t>(k) * a.stride + t];
+    const int64_t rmax = a.rows[k] - 1;
+    keys[i] = a.off[k] + (v < 0 ? 0 : (v > rmax ? rmax : v));
+}
+
+__global__ void td_empty_info(int64_t *info, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) info[i] = 0;
+}
+
+struct TdLayout {
+    bool fast;  // the two-launch table path (else: keys, then the generic key half + bounds)
+    size_t srow, tmp_a, tmp_b, slot, gstart, gsize, ucount;  // fast path
+    size_t keys, inv;                                   // generic path, then its DedupLayout
+    DedupLayout dl;
+    size_t total;
+};
+
+// Fills the table description of a and returns the workspace layout for it.
+int td_setup(TdArgs &a, const int64_t *idx, int64_t stride, int64_t n, int32_t nt,
+             const int64_t *table_rows, TdLayout *out) {
+    ME_CHECK_ARG(n >= 0 && nt >= 1 && nt <= ME_MAX_TABLES, "bad n / n_tables");
+    ME_CHECK_ARG(n * nt < (int64_t{1} << 31), "n * n_tables = %lld too large", (long long)(n * nt));
+    ME_CHECK_ARG(table_rows != nullptr, "table_rows is null");
+    ME_CHECK_ARG(stride >= n, "idx_table_stride %lld < n %lld", (long long)stride, (long long)n);
+    a.idx = idx;
+    a.stride = stride;
+    a.n = static_cast<uint32_t>(n);
+    a.nt = nt;
+    bool fast = n <= kTdMaxN;
+    const int64_t target = std::max<int64_t>(1, ceil_div(n, kTdPartTarget));
+    int64_t off = 0;
+    uint32_t ng = 0;
+    for (int k = 0; k < nt; ++k) {
+        ME_CHECK_ARG(table_rows[k] >= 1, "table %d has %lld rows", k, (long long)table_rows[k]);
+        a.rows[k] = table_rows[k];
+        a.off[k] = off;
+        off += table_rows[k];
+        fast = fast && table_rows[k] <= (int64_t{1} << 32);
+        a.shift[k] = td_shift(table_rows[k], target);
+        a.gbase[k] = ng;
+        ng += static_cast<uint32_t>(((table_rows[k] - 1) >> a.shift[k]) + 1);
+    }
+    a.gbase[nt] = ng;
+    a.ngroups = ng;
+    const int64_t N = n * nt;
+    auto up = [](size_t x) { return (x + 255) & ~size_t{255}; };
+    TdLayout l{};
+    l.fast = fast;
+    size_t o = 0;
+    if (fast) {
+        l.srow = o; o += up(static_cast<size_t>(N) * 4);
+        l.tmp_a = o; o += up(static_cast<size_t>(N) * 8);
+        l.tmp_b = o; o += up(static_cast<size_t>(N) * 8);
+        l.slot = o; o += up(static_cast<size_t>(ng) * kTdCap * 8);
+        l.gstart = o; o += up(static_cast<size_t>(ng) * 4);
+        l.gsize = o; o += up(static_cast<size_t>(ng) * 4);
+        l.ucount = o; o += up(static_cast<size_t>(ng) * 4);
+    } else {
+        l.keys = o; o += up(static_cast<size_t>(N) * 8);
+        l.inv = o; o += up(static_cast<size_t>(N) * 8);  // the inverse when the caller wants none
+        l.dl = dedup_layout(N);
+        o += l.dl.total;
+    }
+    l.total = o;
+    *out = l;
+    return ME_OK;
+}
+}  // namespace
+}  // namespace me
+
+extern "C" int me_dedup_tables_workspace_size(int64_t n, int32_t n_tables, const int64_t *table_rows,
+                                              size_t *bytes) {
+    ME_CHECK_ARG(bytes != nullptr, "bytes is null");
+    TdArgs a{};
+    TdLayout l{};
+    const int st = td_setup(a, nullptr, n, n, n_tables, table_rows, &l);
+    if (st != ME_OK) return st;
+    *bytes = l.total;
+    return ME_OK;
+}
+
+extern "C" int me_dedup_tables(const int64_t *idx, int64_t idx_table_stride, int64_t n, int32_t n_tables,
+                               const int64_t *table_rows, int64_t *uniq, int64_t *local_rows, int64_t *inv,
+                               int64_t *info, void *plan, size_t plan_size, void *workspace,
+                               size_t workspace_size, void *stream) {
+    TdArgs a{};
+    TdLayout l{};
+    const int st = td_setup(a, idx, idx_table_stride, n, n_tables, table_rows, &l);
+    if (st != ME_OK) return st;
+    ME_CHECK_ARG(info != nullptr, "info is null");
+    hipStream_t s = as_stream(stream);
+    if (n == 0) {
+        hipLaunchKernelGGL(td_empty_info, dim3(1), dim3(64), 0, s, info, n_tables + 2);
+        return check_launch("me_dedup_tables");
+    }
+    ME_CHECK_ARG(idx && uniq && local_rows, "null tensor pointer");
+    const int64_t N = n * n_tables;
+    const PlanLayout p = plan_layout(N);
+    if (plan == nullptr || plan_size < p.total) {
+        set_error("me_dedup_tables: plan of %zu bytes needed, got %zu", p.total, plan_size);
+        return ME_ERR_WORKSPACE;
+    }
+    if (workspace == nullptr || workspace_size < l.total) {
+        set_error("me_dedup_tables: workspace of %zu bytes needed, got %zu", l.total, workspace_size);
+        return ME_ERR_WORKSPACE;
+    }
+    uint8_t *pl = static_cast<uint8_t *>(plan);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    a.spos = reinterpret_cast<uint32_t *>(pl + p.spos);
+    a.seg_start = reinterpret_cast<uint32_t *>(pl + p.seg_start);
+    a.seg_pos = reinterpret_cast<uint32_t *>(pl + p.seg_pos);
+    a.uniq = uniq;
+    a.local = local_rows;
+    a.inv = inv;
+    a.info = info;
+    if (l.fast) {
+        a.srow = reinterpret_cast<uint32_t *>(ws + l.srow);
+        a.tmp_a = reinterpret_cast<uint64_t *>(ws + l.tmp_a);
+        a.tmp_b = reinterpret_cast<uint64_t *>(ws + l.tmp_b);
+        a.slot = reinterpret_cast<uint64_t *>(ws + l.slot);
+        a.gstart = reinterpret_cast<uint32_t *>(ws + l.gstart);
+        a.gsize = reinterpret_cast<uint32_t *>(ws + l.gsize);
+        a.ucount = reinterpret_cast<uint32_t *>(ws + l.ucount);
+        const bool vec2 = reinterpret_cast<uintptr_t>(idx) % 16 == 0 && idx_table_stride % 2 == 0 && n % 2 == 0;
+        const int rounds = static_cast<int>(ceil_div(n, 2 * kThreads));
+        const dim3 grid(a.ngroups), block(kThreads);
+#define ME_TD_PART(R)                                                                   \
+    if (rounds <= R) {                                                                  \
+        if (vec2) hipLaunchKernelGGL((td_part<R, true>), grid, block, 0, s, a);         \
+        else hipLaunchKernelGGL((td_part<R, false>), grid, block, 0, s, a);             \
+    } else
+        ME_TD_PART(1) ME_TD_PART(2) ME_TD_PART(4) ME_TD_PART(8) ME_TD_PART(16) ME_TD_PART(32) {}
+#undef ME_TD_PART
+        hipLaunchKernelGGL(td_emit, dim3(a.ngroups), dim3(kThreads), 0, s, a);
+        return check_launch("me_dedup_tables");
+    }
+    // more tokens than the table path takes: the keys, the generic key half, the bounds
+    int64_t *keys = reinterpret_cast<int64_t *>(ws + l.keys);
+    hipLaunchKernelGGL(td_keys, dim3(static_cast<unsigned>(ceil_div(N, kThreads))), dim3(kThreads), 0, s, a,
+                       keys);
+    const int64_t key_bound = a.off[n_tables - 1] + a.rows[n_tables - 1];
+    int64_t *inv_out = inv != nullptr ? inv : reinterpret_cast<int64_t *>(ws + l.inv);
+    const int st2 = dedup_keys_run(keys, N, key_bound, uniq, inv_out, info, a.spos, a.seg_start, a.seg_pos,
+                                   ws + (l.inv + ((static_cast<size_t>(N) * 8 + 255) & ~size_t{255})), l.dl,
+                                   s);
+    if (st2 != ME_OK) return st2;
+    TableOffsets t{};
+    for (int k = 0; k < n_tables; ++k) t.off[k] = a.off[k];
+    t.off[n_tables] = key_bound;
+    hipLaunchKernelGGL(table_bounds_kernel, dim3(static_cast<unsigned>(ceil_div(N + 1, kThreads))),
+                       dim3(kThreads), 0, s, uniq, N, info, t, n_tables, local_rows, info);
+    return check_launch("me_dedup_tables (generic)");
 }
 
 extern "C" int me_dedup_sums(const void *plan, size_t plan_size, int64_t n, const int64_t *count,

@@ -778,6 +778,31 @@ def dedup_table_bounds(uniq, count, offsets):
     return local, info
 
 
+def dedup_tables(idx2d, table_rows, inverse=True):
+    """[uniq, local rows, inv, count, plan, info] of the token-major lookups of per-table row ids
+    idx2d [n_tables, n] (key offset_k + idx2d[k, t] at position t * n_tables + k): what
+    dedup_keys of those keys and dedup_table_bounds of its unique keys give (torch.unique of
+    micro_engram/rows.py:81 and the table slices of rows.py:123-129), in two launches. count is
+    info[:1]; info = [count, first unique index of each table, count]. inverse=False leaves inv
+    unwritten (the segment sums do not read it) and saves its scattered writes."""
+    dev = require_gpu(idx2d)
+    if idx2d.dtype != torch.int64 or idx2d.stride(1) != 1:
+        idx2d = idx2d.long().contiguous()
+    nt, n = idx2d.shape
+    N = n * nt
+    rows = i64_array([int(r) for r in table_rows])
+    ints = torch.empty(3 * N + nt + 2, dtype=torch.int64, device=dev)  # four outputs, one allocation
+    uniq, local, inv, info = ints[:N], ints[N:2 * N], ints[2 * N:3 * N], ints[3 * N:]
+    plan = torch.empty(max(dedup_plan_bytes(N), 16), dtype=torch.uint8, device=dev)
+    size = ctypes.c_size_t(0)
+    call("me_dedup_tables_workspace_size", n, nt, rows, ctypes.byref(size))
+    ws = torch.empty(max(size.value, 16), dtype=torch.uint8, device=dev)
+    call("me_dedup_tables", idx2d.data_ptr() if N else None, idx2d.stride(0) if n else 0, n, nt, rows,
+         _p(uniq) if N else None, _p(local) if N else None, _p(inv) if N and inverse else None, info.data_ptr(),
+         plan.data_ptr(), plan.numel(), ws.data_ptr(), ws.numel(), stream_of(dev))
+    return [uniq, local, inv, info[:1], plan, info]
+
+
 def dedup_sums(plan, count, grads):
     """fp32 [n, D]: row u = the index_add_ sum of the gradient rows of unique key u (rows.py:117-118),
     from the plan and count of dedup_keys on the same n keys; rows past the count are unset."""

@@ -109,10 +109,9 @@ class _KeyPlan:
 
     def make(self):
         if self.outs is None:
-            offs_all = _offsets_on(self.offsets, self.idx2d.device)
-            keys = _lookup_keys(self.idx2d, offs_all[:-1])
-            self.outs = ops.dedup_keys(keys, int(self.offsets[-1]))
-            self.local_all, info = ops.dedup_table_bounds(self.outs[0], self.outs[2], self.offsets)
+            rows = [b - a for a, b in zip(self.offsets, self.offsets[1:])]
+            uniq, self.local_all, inv, count, plan, info = ops.dedup_tables(self.idx2d, rows, inverse=False)
+            self.outs = [uniq, inv, count, plan]  # inv unwritten: the segment sums read the plan
             self.host = _pinned_take(info.numel())
             self.host.copy_(info, non_blocking=True)
             self.ready = torch.cuda.Event()
