@@ -37,7 +37,8 @@ all inputs already in HBM. Prints one JSON line:
                 exist (segment sums of the 196,608 lookups' gradient rows + row-wise Adam with
                 stochastic rounding on the touched rows), algorithmic bytes / duration (graph
                 replay) over 16 distinct batches; the key plan the sums read (unique keys,
-                inverse, segment bounds) is made in the forward from the row ids and is timed
+                their rows and segment bounds, the tables' bounds) is made in the forward from
+                the per-table row ids (me_dedup_tables, as the row lookup calls it) and is timed
                 beside it (key_plan_ms; with_key_plan_frac counts all three)
   training_step  one training step of a second engram of the same shape with row-sharded
                 tables (sparse row gradients): forward with gradients, backward from a fixed
@@ -127,7 +128,7 @@ def update_batches(eng, dev, n_batches):
         bounds = torch.searchsorted(uniq[:n_uniq], torch.tensor(offs, device=dev)).tolist()
         rows = [uniq[bounds[k]:bounds[k + 1]] - offs[k] for k in range(len(eng.tables))]
         sums = [gsum[bounds[k]:bounds[k + 1]] for k in range(len(eng.tables))]
-        out.append((keys, grads, rows, sums, n_uniq, plan, count))
+        out.append((keys, grads, rows, sums, n_uniq, plan, count, idx))
     return out, offs[-1]
 
 
@@ -141,13 +142,13 @@ def key_bound_offsets(eng):
 
 def update_bytes(n_lookups, n_uniq, dim, esize):
     """Algorithmic bytes of one sparse update, in three parts.
-    Key plan (in the forward, from the row ids): read the int64 keys; write the unique keys,
-    the int64 inverse, the sorted positions (4 B per lookup) and two 4-byte segment bounds per
-    unique key. Segment sums (the backward): read the fp32 gradient rows and their sorted
+    Key plan (in the forward, from the per-table row ids): read the int64 row ids; write the
+    unique keys and their int64 rows, the sorted positions (4 B per lookup) and two 4-byte segment
+    bounds per unique key. Segment sums (the backward): read the fp32 gradient rows and their sorted
     positions, the segment bounds; write the summed fp32 rows. Row-wise Adam per unique row:
     weight and first moment read and written (esize each), the fp32 second moment read and
     written, the summed gradient and the row id read (784 B for 64 bf16)."""
-    keys = n_lookups * 8 + n_uniq * 8 + n_lookups * 8 + n_lookups * 4 + n_uniq * 8
+    keys = n_lookups * 8 + n_uniq * 8 + n_uniq * 8 + n_lookups * 4 + n_uniq * 8
     sums = n_lookups * (4 * dim + 4) + n_uniq * (8 + 4 * dim)
     adam = n_uniq * (4 * dim * esize + 8 + 4 * dim + 8)
     return keys, sums, adam
@@ -692,15 +693,15 @@ def main():
         exp_avg_sqs = [torch.zeros(t.shape[0], device=dev) for t in tables]
         streams = list(range(len(tables)))
 
-        def dedup_keys(k):
-            ops.dedup_keys(ubatches[k % CYCLE][0], key_bound)
+        def dedup_keys(k):  # the row lookup's key plan: per-table row ids, no inverse
+            ops.dedup_tables(ubatches[k % CYCLE][7], eng.table_rows, inverse=False)
 
         def dedup_sums(k):
-            _, grads, _, _, _, plan, count = ubatches[k % CYCLE]
+            _, grads, _, _, _, plan, count, _ = ubatches[k % CYCLE]
             ops.dedup_sums(plan, count, grads)
 
         def adam(k):
-            _, _, rows, sums, _, _, _ = ubatches[k % CYCLE]
+            _, _, rows, sums, _, _, _, _ = ubatches[k % CYCLE]
             ops.sparse_adam(tables, exp_avgs, exp_avg_sqs, rows, sums, [1] * len(tables),
                             streams, lr=5e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
                             rowwise=True, lazy=True, stochastic_rounding=True, seed=2024)
@@ -794,8 +795,9 @@ def main():
         "roofline_update": {
             "kernel": "sparse update after the backward: segment sums of the gradient rows + "
                       "row-wise Adam with stochastic rounding (the key plan -- unique keys, "
-                      "inverse, segment bounds -- runs in the training forward, after the "
-                      "gate's launches on the same stream; its time is key_plan_ms)",
+                      "their rows, segment bounds, table bounds, from the per-table row ids -- "
+                      "runs in the training forward, after the gate's launches on the same "
+                      "stream; its time is key_plan_ms)",
             "bound": "hbm",
             "achieved": update_gbs,
             "peak": HBM_PEAK_GBS,

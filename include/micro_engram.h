@@ -353,7 +353,7 @@ int me_dedup_table_bounds(const int64_t *uniq, int64_t n, const int64_t *count,
 /*
  * me_dedup_tables -- the key half of a row lookup's dedup from its per-table row ids, and the
  * tables' bounds in it: what me_dedup_keys + me_dedup_table_bounds give for the token-major keys
- * offset_k + idx[k][t] (lookup position t * n_tables + k), in two launches for up to 16,384
+ * offset_k + idx[k][t] (lookup position t * n_tables + k), in two launches for up to 8,192
  * tokens (micro_engram/rows.py:81 torch.unique(return_inverse=True) over the lookups' keys, and
  * the per-table slices of rows.py:123-129). Every table holds n lookups, so table k's part of the
  * sorted order is [k * n, (k + 1) * n): each workgroup takes one range of one table's rows, reads

@@ -719,16 +719,18 @@ __global__ __launch_bounds__(kThreads) void gd_emit(const uint64_t *comp, const 
 // exchange between workgroups; only the unique numbering needs the earlier parts' unique counts,
 // which is the second launch:
 //   td_part  per (table, part): the table's ids read once (two per thread per round of 512
-//            tokens, kept in registers), the part's (row, token) composites compacted in token
-//            order into LDS (wave ballots, then one scan of the per-(round, wave) counts), ranked
-//            inside 1024 buckets of their top row bits, and written at the part's place: spos
-//            (the position) and srow (the row); its size, place and unique count into gsize,
-//            gstart and ucount. A part larger than LDS sorts in global memory (stable LSD radix).
+//            tokens, all loads in flight) and kept as rows in LDS; one block scan counts the
+//            part's lookups and the lookups of lower parts and gives each thread the slots of its
+//            own, which it fills by walking its match bits; the composites (row in part, token)
+//            are ranked inside 1024 buckets of their top row bits and written at the part's
+//            place: spos (the position), and a slot copy (position, row) for td_emit; its size,
+//            place and unique count into gsize, gstart and ucount. A part larger than LDS sorts
+//            in global memory (stable LSD radix) and leaves its rows in srow.
 //   td_emit  per (table, part): its unique keys numbered after the earlier parts' (a block sum
 //            of their unique counts), then uniq, local rows, inv, the segment plan and the
 //            table bounds (info = [count, first unique index of each table, count]).
-constexpr uint32_t kTdMaxN = 16384;           // tokens per table this path takes
-constexpr int kTdRounds = kTdMaxN / (2 * kThreads);
+constexpr uint32_t kTdMaxN = 8192;            // tokens per table this path takes
+constexpr int kTdRounds = kTdMaxN / (2 * kThreads);  // 16: a thread's match bits fit 32
 constexpr int kTdCap = 2048;                  // composites a part sorts in LDS
 constexpr int kTdBucketBits = 10;
 constexpr int kTdBuckets = 1 << kTdBucketBits;
@@ -770,6 +772,7 @@ __global__ __launch_bounds__(kThreads) void td_part(const TdArgs a) {
     __shared__ uint32_t s_cur[kTdBuckets];     // bucket fill counters
     __shared__ uint32_t s_wtot[kThreads / 64];
     __shared__ uint32_t s_red[kThreads / 64];
+    __shared__ uint32_t s_rows[kTdMaxN];       // the table's rows, by token
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = blockIdx.x;
     const int k = td_table_of(a, g);
@@ -795,26 +798,31 @@ __global__ __launch_bounds__(kThreads) void td_part(const TdArgs a) {
             v[r][1] = t0 + 1 < n ? ids[t0 + 1] : 0;
         }
     }
-    // bit 2r + h of `match`: a lookup of this part; counts of this part's and of lower parts'
-    uint32_t row[kRounds][2];
-    uint64_t match = 0;
+    // each token's row (clamped) into LDS; bit 2r + h of `match` marks a lookup of this part
+    // (kRounds <= 16: 32 bits); counts of this part's lookups and of lower parts'. A token past
+    // n gets part ~0, which counts as neither.
+    uint32_t match = 0;
     uint32_t cm = 0, cl = 0;
+    const uint32_t rmax32 = static_cast<uint32_t>(rmax);
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
+        uint32_t rw[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t t = static_cast<uint32_t>(r * 2 * kThreads + 2 * tid + h);
-            const int64_t x = v[r][h];
-            row[r][h] = static_cast<uint32_t>(x < 0 ? 0 : (x > rmax ? rmax : x));
-            const uint32_t p = row[r][h] >> sh;
-            const bool valid = t < n;
-            const bool m = valid && p == part;
-            cm += m ? 1u : 0u;
-            cl += (valid && p < part) ? 1u : 0u;
-            match |= m ? (1ull << (2 * r + h)) : 0ull;
+            const uint64_t x = static_cast<uint64_t>(v[r][h]);
+            const uint32_t hi = static_cast<uint32_t>(x >> 32), lo = static_cast<uint32_t>(x);
+            rw[h] = hi == 0u ? min(lo, rmax32) : (static_cast<int32_t>(hi) < 0 ? 0u : rmax32);
+            const uint32_t p = t < n ? rw[h] >> sh : ~0u;
+            const uint32_t mt = p == part ? 1u : 0u;
+            cm += mt;
+            cl += p < part ? 1u : 0u;
+            match |= mt << (2 * r + h);
         }
+        const uint32_t t0 = static_cast<uint32_t>(r * 2 * kThreads + 2 * tid);
+        if (t0 < n) *reinterpret_cast<u32x2_v *>(&s_rows[t0]) = u32x2_v{rw[0], rw[1]};
     }
-    // both counts in one block scan (each below 2^16: at most n <= 16384 of either); the low half
+    // both counts in one block scan (each below 2^16: at most n <= 8192 of either); the low half
     // of this thread's exclusive prefix is where its own lookups of the part go
     uint32_t tot;
     const uint32_t pre = block_exclusive_scan((cl << 16) | cm, s_wtot, &tot);
@@ -823,20 +831,16 @@ __global__ __launch_bounds__(kThreads) void td_part(const TdArgs a) {
     const bool in_lds = m <= static_cast<uint32_t>(kTdCap);
     uint64_t *gbuf = a.tmp_a + start;
     // ---- the part's composites (row in part << 32 | token), each thread's at its own slots, in
-    // no particular order (the sort below orders whole composites)
+    // no particular order (the sort below orders whole composites): one pass over the set bits
     const uint32_t lmask = (1u << sh) - 1u;
     uint32_t dst = pre & 0xffffu;
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if ((match >> (2 * r + h)) & 1ull) {
-                const uint32_t t = static_cast<uint32_t>(r * 2 * kThreads + 2 * tid + h);
-                const uint64_t c = (static_cast<uint64_t>(row[r][h] & lmask) << 32) | t;
-                if (in_lds) s_a[dst] = c; else gbuf[dst] = c;
-                ++dst;
-            }
-        }
+    while (match != 0u) {
+        const int bit = __builtin_ctz(match);
+        match &= match - 1u;
+        const uint32_t t = static_cast<uint32_t>((bit >> 1) * 2 * kThreads + 2 * tid + (bit & 1));
+        const uint64_t c = (static_cast<uint64_t>(s_rows[t] & lmask) << 32) | t;
+        if (in_lds) s_a[dst] = c; else gbuf[dst] = c;
+        ++dst;
     }
     __syncthreads();
     if (in_lds) {
@@ -1996,7 +2000,7 @@ extern "C" int me_dedup_tables(const int64_t *idx, int64_t idx_table_stride, int
         if (vec2) hipLaunchKernelGGL((td_part<R, true>), grid, block, 0, s, a);         \
         else hipLaunchKernelGGL((td_part<R, false>), grid, block, 0, s, a);             \
     } else
-        ME_TD_PART(1) ME_TD_PART(2) ME_TD_PART(4) ME_TD_PART(8) ME_TD_PART(16) ME_TD_PART(32) {}
+        ME_TD_PART(1) ME_TD_PART(2) ME_TD_PART(4) ME_TD_PART(8) ME_TD_PART(16) {}
 #undef ME_TD_PART
         hipLaunchKernelGGL(td_emit, dim3(a.ngroups), dim3(kThreads), 0, s, a);
         return check_launch("me_dedup_tables");
