@@ -91,3 +91,18 @@ def test_dedup_tables_empty():
     uniq, local, inv, count, plan, info = ops.dedup_tables(torch.empty(3, 0, dtype=torch.long, device=DEV),
                                                            [5, 6, 7])
     assert info.cpu().tolist() == [0, 0, 0, 0, 0]
+
+
+def test_dedup_tables_hot_buckets():
+    # rows repeated 49 to 600 times among random ones: buckets far larger than their share of
+    # the part, ranked in LDS (the part still fits)
+    n, rows = 8192, 1 << 22
+    g = torch.Generator().manual_seed(11)
+    idx = torch.randint(0, rows, (2, n), generator=g)
+    perm = torch.randperm(n, generator=g)
+    at = 0
+    for reps, row in ((49, 7), (100, 300_001), (300, 900_000), (512, 1_500_000), (513, 2_900_000), (600, 4_000_000)):
+        idx[0, perm[at:at + reps]] = row
+        at += reps
+    idx[1, perm[:300]] = 123  # a second table with one hot row
+    _check(idx, [rows, rows])
