@@ -101,7 +101,13 @@ struct Chunk<2> {
 };
 
 // GATHER = false: hash only (no memory vectors), its own instantiation without phase 3.
-template <int MODE, int VEC, bool GATHER>
+// PACED: at most two of a thread's row loads in flight, for launches of 8 tokens per workgroup
+// (six chunks per thread) that are one round of resident workgroups. Measured on MI355X: the
+// 8192-token prefill gather 12.4-12.5 us paced against 12.7-13.0 with all six in flight (every
+// workgroup's requests queue at once, and fewer random-row requests queued together are served
+// faster); launches of several rounds (65,536 tokens: 79.7 against 74 us) and those of 1-4
+// tokens per workgroup (0.1-0.25 us) are faster unpaced.
+template <int MODE, int VEC, bool GATHER, bool PACED = false>
 __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
     using V = typename Chunk<VEC>::T;
     __shared__ int64_t s_tok[64 * ME_MAX_ORDER];  // [tpb][max_order] hashed token values
@@ -226,6 +232,7 @@ __global__ __launch_bounds__(kBlock) void lookup_kernel(const LookupArgs a) {
         for (int u = 0; u < kUnroll; ++u) {
             v[u] = V{};
             if (src[u] != 0) v[u] = *as_global_addr<const V>(src[u]);
+            if (PACED && u % 2 == 1 && u + 1 < kUnroll) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -304,6 +311,8 @@ int fill_gather(LookupArgs &a, const void *const *tables, int32_t dim, int dtype
 // Workgroups a launch keeps when its tokens allow: fewer tokens per workgroup for small batches
 // (a 256-token decode step, the 2048-token fp32 case) so that every CU gets work.
 constexpr int64_t kMinBlocks = 512;
+// Largest launch that takes the paced copy (one round: every workgroup resident at once).
+constexpr unsigned kPacedMaxBlocks = 2048;
 
 template <int MODE>
 int launch(const LookupArgs &a0, int vec, hipStream_t stream, const char *what) {
@@ -314,6 +323,10 @@ int launch(const LookupArgs &a0, int vec, hipStream_t stream, const char *what) 
     const dim3 grid(static_cast<unsigned>(ceil_div(a.n, a.tpb)));
     if (a.mem == nullptr) {
         hipLaunchKernelGGL((lookup_kernel<MODE, 16, false>), grid, dim3(kBlock), 0, stream, a);
+        return check_launch(what);
+    }
+    if (vec == 16 && a.tpb >= 8 && grid.x <= kPacedMaxBlocks) {
+        hipLaunchKernelGGL((lookup_kernel<MODE, 16, true, true>), grid, dim3(kBlock), 0, stream, a);
         return check_launch(what);
     }
     switch (vec) {

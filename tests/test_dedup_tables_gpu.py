@@ -106,3 +106,12 @@ def test_dedup_tables_hot_buckets():
         at += reps
     idx[1, perm[:300]] = 123  # a second table with one hot row
     _check(idx, [rows, rows])
+
+
+def test_dedup_tables_calls_in_a_row():
+    # plans of more and fewer parts back to back on one stream, each against the oracle
+    g = torch.Generator().manual_seed(21)
+    cases = [(4096, [1 << 22] * 6), (512, [1 << 20, 77]), (4096, [1 << 22] * 6), (2000, [5000, 1 << 21, 3])]
+    for n, rows in cases:
+        idx = torch.stack([torch.randint(0, r, (n,), generator=g) for r in rows])
+        _check(idx, rows, dim=2)
