@@ -91,12 +91,12 @@ def parse():
     return ap.parse_args()
 
 
-# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,433.5
-# KiB per dispatch, x2.0) and WRITE_SIZE (24,588.0 KiB, x1.0), the factors being what the two
+# HBM bytes per launch of the gather kernel on this workload: rocprofv3 --pmc FETCH_SIZE (12,433.1
+# KiB per dispatch, x2.0) and WRITE_SIZE (24,600.7 KiB, x1.0), the factors being what the two
 # counters read for this script's device copy of the gather's output size. A counter run cannot
 # share a process with the timing, so the figure is a measured constant, re-measured when the
-# kernel or its inputs change (the canon map's lines are in it).
-GATHER_TRAFFIC_BYTES = 50_641_920
+# kernel or its inputs change (the canon map's lines are in it; the paced row loads).
+GATHER_TRAFFIC_BYTES = 50_654_105
 CYCLE = 16  # distinct prefill batches the timed steps cycle through
 
 
