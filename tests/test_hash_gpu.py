@@ -129,11 +129,12 @@ def test_hash_gather_equals_hash_then_gather():
     assert torch.equal(mem, torch.cat(eng.lookup(list(ref_idx.unbind(0))), dim=-1).reshape(100, -1))
 
 
-@pytest.mark.parametrize("n", [1, 700, 1025, 2049, 4089, 4096])
+@pytest.mark.parametrize("n", [1, 700, 1025, 2049, 4089, 4096, 16384, 16393])
 def test_gathers_across_tokens_per_workgroup(n):
     # the launches give each workgroup 8 tokens (24 tables), fewer when that would leave under
-    # 512 workgroups (n < 4089: 4, 2 or 1 per workgroup): every size is bit-exact against the
-    # oracle, whole and ragged last workgroups included
+    # 512 workgroups (n < 4089: 4, 2 or 1 per workgroup), and pace their row loads while they
+    # are one round of 2048 workgroups (16384 tokens; 16393 is past it): every size is bit-exact
+    # against the oracle, whole and ragged last workgroups included
     eng = _engram(orders=(2, 3, 4), heads=8, dim=64, dtype=torch.bfloat16, sizes={2: 4001, 3: 7919, 4: 6007},
                   canon=torch.randint(0, 1000, (1000,), generator=torch.Generator().manual_seed(n)))
     gen = torch.Generator().manual_seed(n)
